@@ -1,0 +1,143 @@
+/*
+ * vdx_sampler.h -- C ABI of libvdxsampler.so, the MI355X (gfx950) token
+ * sampler of VindexLLM.
+ *
+ * Drop-in boundary for TVdxSampler (src/VindexLLM.Sampler.pas:37-91 in the
+ * reference).  Logits stay in HBM: the batched entry point samples B rows of
+ * device-resident fp32 logits with hand-written HIP kernels and writes B
+ * token ids, without a host round trip.  Every type is plain C (pointers,
+ * fixed-width integers); `stream` is a hipStream_t passed as void*.
+ *
+ * Return codes: 0 = OK, negative = error (see VDX_E_*); the message is in
+ * vdx_sampler_last_error().  No entry point falls back to the CPU.
+ */
+#ifndef VDX_SAMPLER_H
+#define VDX_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VDX_OK 0
+#define VDX_E_INVALID_ARG (-1)
+#define VDX_E_HIP (-2)            /* HIP runtime / device error            */
+#define VDX_E_UNSUPPORTED (-3)    /* configuration outside the GPU kernels */
+#define VDX_E_NO_MEMORY (-4)
+
+/* RNG used for the one uniform each non-greedy row consumes per call. */
+#define VDX_RNG_XOSHIRO 0  /* reference stream (Sampler.pas:192-248); row r is
+                              seeded as a reference sampler with Seed + r    */
+#define VDX_RNG_PHILOX 1   /* counter-based Philox4x64-10: word 0 of block
+                              {step,row,0,0} under key {Seed,0}; (x>>40)/2^24 */
+
+/* Per-row diagnostic flags written to vdx_sample_outputs.flags. */
+#define VDX_ROW_GREEDY 0x1
+#define VDX_ROW_TOPK_FAST 0x2     /* exact top-K without slot-order replay   */
+#define VDX_ROW_TOPK_REPLAY 0x4   /* exact reference min-buffer replay       */
+#define VDX_ROW_FULL 0x8          /* K <= 0 or K >= V full-softmax path      */
+#define VDX_ROW_NAN 0x10          /* row held NaN (or inf) handled literally */
+#define VDX_ROW_FALLBACK 0x20     /* no cumulative weight exceeded t         */
+
+/* TVdxSamplerConfig (src/VindexLLM.Sampler.pas:26-34), bit-identical to the
+ * Pascal record under {$A8} (src/VindexLLM.Defines.inc:13): 32 bytes,
+ * offsets 0,4,8,12,16,20,24. */
+typedef struct vdx_sampler_config {
+  float temperature;     /* 0 = greedy argmax, > 0 = divide logits by it     */
+  int32_t top_k;         /* 0 = disabled (full softmax), > 0 = keep top K     */
+  float top_p;           /* 1 = disabled, < 1 = nucleus (top-K path only)     */
+  float min_p;           /* 0 = disabled, > 0 = floor relative to top prob    */
+  float repeat_penalty;  /* 1 = disabled                                      */
+  int32_t repeat_window; /* history ring length per row                       */
+  int64_t seed;          /* 0 = timer seed, > 0 deterministic                 */
+} vdx_sampler_config;
+
+typedef struct vdx_sampler vdx_sampler;
+
+/* Optional outputs of vdx_sampler_process_device.  Every pointer is device
+ * memory and may be NULL.  topk_* hold `topk_stride` entries per row (>= K)
+ * in descending (value, then lower index) order; topk_prob is the final
+ * normalised probability (0 for entries cut by Min-P / Top-P). */
+typedef struct vdx_sample_outputs {
+  int32_t *tokens;     /* [rows]                    */
+  int32_t *topk_idx;   /* [rows * topk_stride]      */
+  float *topk_prob;    /* [rows * topk_stride]      */
+  int32_t topk_stride;
+  uint32_t *flags;     /* [rows] VDX_ROW_*          */
+  float *uniforms;     /* [rows] the uniform each row consumed (0 if greedy) */
+} vdx_sample_outputs;
+
+/* TVdxSampler.DefaultConfig (Sampler.pas:100-109). */
+void vdx_sampler_default_config(vdx_sampler_config *out);
+
+/* TVdxSampler.Create (Sampler.pas:111-122): default config, a RepeatWindow
+ * ring per row, PRNG seeded from the timer (Seed = 0).  `max_rows` bounds
+ * the batch of every later call; device memory is allocated here and grown
+ * (outside the sampling call) when a larger vocabulary is first seen. */
+int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows);
+
+/* TVdxSampler.Destroy (Sampler.pas:124-130). */
+void vdx_sampler_destroy(vdx_sampler *s);
+
+/* TVdxSampler.SetConfig (Sampler.pas:132-150): a RepeatWindow change resizes
+ * and clears every row's history; a Seed change reseeds every row. */
+int vdx_sampler_set_config(vdx_sampler *s, const vdx_sampler_config *cfg);
+
+/* TVdxSampler.GetConfig (Sampler.pas:152-155). */
+int vdx_sampler_get_config(const vdx_sampler *s, vdx_sampler_config *out);
+
+/* TVdxSampler.Process (Sampler.pas:265-528) for one host-resident row, as
+ * called by TVdxInference.RunUnembedding (Inference.pas:327-339): uploads the
+ * row, samples it on the GPU (row 0's history and RNG), writes the
+ * penalised logits back into `logits` (the reference mutates its input) and
+ * returns the token id (>= 0) or a negative error code. */
+int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab);
+
+/* Batched, device-resident Process: row r of `logits` starts at
+ * logits + r*row_stride (fp32, device memory, mutated in place by the
+ * repetition penalty exactly as Sampler.pas:285-303).  `uniforms` (device,
+ * nullable) injects the per-row uniform in [0,1) that replaces the RNG draw
+ * (the RNG is then not advanced); NULL draws from the sampler's RNG.
+ * Stream-ordered and asynchronous; allocates nothing once the workspace
+ * covers `vocab`.  Rows must not alias. */
+int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows,
+                               int32_t vocab, int64_t row_stride,
+                               const float *uniforms,
+                               const vdx_sample_outputs *out, void *stream);
+
+/* TVdxSampler.AddToHistory (Sampler.pas:530-539) for one row. */
+int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token);
+
+/* AddToHistory for rows [0, rows) from device-resident token ids, as the
+ * generation loop does after each step (Inference.pas:653). */
+int vdx_sampler_add_to_history_device(vdx_sampler *s, const int32_t *tokens,
+                                      int32_t rows, void *stream);
+
+/* TVdxSampler.ResetHistory (Sampler.pas:541-549) for one row (row < 0: all
+ * rows): clears the ring and reseeds that row only when Seed > 0. */
+int vdx_sampler_reset_history(vdx_sampler *s, int32_t row);
+
+/* Replaces a row's history ring (count ids in array order, next write
+ * position `pos`); the reference has no bulk setter -- this restores a saved
+ * ring (sampler-state checkpoint). */
+int vdx_sampler_set_history(vdx_sampler *s, int32_t row, const int32_t *ids,
+                            int32_t count, int32_t pos);
+
+/* Reads a row's history ring back (up to `cap` ids); returns the count. */
+int32_t vdx_sampler_get_history(vdx_sampler *s, int32_t row, int32_t *ids,
+                                int32_t cap, int32_t *pos);
+
+/* Selects VDX_RNG_XOSHIRO (default) or VDX_RNG_PHILOX; reseeds all rows. */
+int vdx_sampler_set_rng(vdx_sampler *s, int32_t kind);
+
+/* Last error message of `s` (or of the last failed create when s is NULL). */
+const char *vdx_sampler_last_error(const vdx_sampler *s);
+
+/* Library version string. */
+const char *vdx_sampler_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,176 @@
+"""Shared helpers of the GPU parity tests: run the HIP sampler and the CPU
+oracle on the same seeded inputs and compare them to the north-star bar:
+tokens identical except draws within 1e-6*S of a CDF boundary (counted),
+top-K index sets and penalised logits bit-exact, probabilities within 1e-5
+relative."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+from oracle import vdx_oracle as O
+
+BOUNDARY_EPS = 1e-6
+PROB_RTOL = 1e-5
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def gpu_sample(logits: np.ndarray, cfg: dict, u: np.ndarray | None, hist=None, topk_out=True,
+               rng_kind=None, seed=None, row_stride=None, offset=0):
+    """Runs one batched call; returns dict(tokens, topk_idx, topk_prob, flags, logits_after,
+    uniforms)."""
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    B, V = logits.shape
+    dev = torch.device("cuda:0")
+    stride = V if row_stride is None else row_stride
+    buf = np.full(offset + B * stride + 8, np.float32(-7.0), dtype=np.float32)
+    for r in range(B):
+        buf[offset + r * stride: offset + r * stride + V] = logits[r]
+    d = torch.from_numpy(buf).to(dev)
+    view = d[offset:]
+    with TVdxSampler(0, B) as s:
+        c = s.DefaultConfig()
+        c.Temperature = cfg.get("temperature", 0.0)
+        c.TopK = cfg.get("top_k", 0)
+        c.TopP = cfg.get("top_p", 1.0)
+        c.MinP = cfg.get("min_p", 0.0)
+        c.RepeatPenalty = cfg.get("repeat_penalty", 1.0)
+        c.RepeatWindow = cfg.get("repeat_window", 64)
+        c.Seed = cfg.get("seed", 0) if seed is None else seed
+        s.SetConfig(c)
+        if rng_kind is not None:
+            s.SetRng(rng_kind)
+        if hist is not None:
+            for r in range(B):
+                s.set_history(r, hist[r])
+        K = max(int(c.TopK), 1)
+        ti = torch.full((B, K), -1, dtype=torch.int32, device=dev) if topk_out else None
+        tp = torch.full((B, K), -1.0, dtype=torch.float32, device=dev) if topk_out else None
+        fl = torch.zeros(B, dtype=torch.int32, device=dev)
+        uo = torch.zeros(B, dtype=torch.float32, device=dev)
+        uu = torch.from_numpy(np.ascontiguousarray(u, dtype=np.float32)).to(dev) if u is not None else None
+        tok = s.process_device(view, uniforms=uu, topk_idx=ti, topk_prob=tp, flags=fl,
+                               uniforms_out=uo, rows=B, vocab=V, row_stride=stride)
+        torch.cuda.synchronize()
+        after = d.cpu().numpy()
+    la = np.stack([after[offset + r * stride: offset + r * stride + V] for r in range(B)])
+    return dict(tokens=tok.cpu().numpy(), topk_idx=ti.cpu().numpy() if topk_out else None,
+                topk_prob=tp.cpu().numpy() if topk_out else None, flags=fl.cpu().numpy(),
+                logits_after=la, uniforms=uo.cpu().numpy())
+
+
+def oracle_rows(logits: np.ndarray, cfg: dict, u: np.ndarray, hist=None):
+    """Per-row oracle results (token, trace, penalised row)."""
+    oc = O.make_config(**{k: v for k, v in cfg.items() if k != "seed"})
+    out = []
+    for r in range(logits.shape[0]):
+        row = logits[r].copy()
+        h = hist[r] if hist is not None else None
+        tok, tr = O.process_row(row, oc, float(u[r]) if u is not None else 0.0, hist=h, trace=True)
+        out.append((tok, tr, row))
+    return out
+
+
+def canonical_topk(tr):
+    """Oracle's final top-K entries in (value desc, index asc) order with the
+    final normalised probability of each."""
+    K = tr.k
+    val = {tr.slot_idx[k]: tr.slot_val[k] for k in range(K)}
+    ent = []
+    for p in range(K):
+        i = tr.order_idx[p]
+        v = np.float32(val[i])
+        q = tr.order_q[p]
+        ent.append((v, i, q))
+
+    def key(e):
+        v = e[0]
+        vv = np.inf if np.isnan(v) else float(v)
+        return (-vv, e[1])
+
+    ent.sort(key=key)
+    S = tr.sum_final
+    idx = [e[1] for e in ent]
+    prob = [float(np.float32(e[2] / S)) if S > 0 else 0.0 for e in ent]
+    return idx, prob
+
+
+def boundary_distance(tr):
+    if tr.sum_final == 0 or not np.isfinite(tr.sum_final):
+        return np.inf
+    return min(tr.target - tr.cdf_lo, tr.cdf_hi - tr.target) / tr.sum_final
+
+
+def compare(g, orc, cfg, check_topk=True, check_logits=True, label=""):
+    """Asserts parity; returns the number of near-boundary draws that differ."""
+    n_boundary = 0
+    B = len(orc)
+    for r in range(B):
+        tok, tr, row = orc[r]
+        if check_logits:
+            assert np.array_equal(g["logits_after"][r].view(np.uint32), row.view(np.uint32)), \
+                f"{label} row {r}: penalised logits differ"
+        if g["tokens"][r] != tok:
+            d = boundary_distance(tr)
+            assert d < BOUNDARY_EPS, (f"{label} row {r}: token {g['tokens'][r]} != oracle {tok} "
+                                      f"(boundary distance {d:.3e}, flags {g['flags'][r]:#x})")
+            n_boundary += 1
+        if check_topk and tr.path == O.PATH_TOPK and g["topk_idx"] is not None:
+            idx, prob = canonical_topk(tr)
+            K = tr.k
+            assert g["topk_idx"][r][:K].tolist() == idx, f"{label} row {r}: top-K set/order differs"
+            gp = g["topk_prob"][r][:K].astype(np.float64)
+            op = np.array(prob, dtype=np.float64)
+            ok = np.abs(gp - op) <= PROB_RTOL * np.abs(op) + 1e-30
+            assert ok.all(), f"{label} row {r}: probabilities differ {gp[~ok][:4]} vs {op[~ok][:4]}"
+    return n_boundary
+
+
+# ---- synthetic inputs of the benchmark configurations ------------------------------------
+def u_stream(rng, B):
+    return (rng.integers(0, 2**24, B) / 2**24).astype(np.float32)
+
+
+def cfg1_logits(rng, B=1, V=262144):
+    L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+    for r in range(B):
+        ids = rng.choice(V, 16, replace=False)
+        L[r, ids] += np.float32(8.0)
+    return L
+
+
+def cfg2_logits(rng, B, V=262144):
+    L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+    for r in range(B):
+        ids = rng.choice(V, 4, replace=False)
+        L[r, ids] = np.float32(L[r].max() + 1.0)
+    return L
+
+
+def cfg3_inputs(rng, B=64, V=262144, H=256):
+    L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+    hist = np.zeros((B, H), dtype=np.int32)
+    for r in range(B):
+        hot = rng.choice(V, 32, replace=False)
+        L[r, hot] += np.float32(6.0)
+        h = np.concatenate([rng.choice(hot, H // 2, replace=True), rng.integers(0, V, H // 2)])
+        rng.shuffle(h)
+        hist[r] = h
+    return L, hist
+
+
+def cfg4_logits(rng, B=256, V=262144):
+    L = np.empty((B, V), dtype=np.float32)
+    lr = np.log(np.arange(1, V + 1, dtype=np.float64))
+    for r in range(B):
+        ranks = rng.permutation(V)
+        L[r] = (-1.1 * lr[ranks] + 0.5 * rng.standard_normal(V)).astype(np.float32)
+    return L

@@ -1,0 +1,92 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/vdx_sampler.h, lays out vdx_sampler_config exactly as the
+Pascal TVdxSamplerConfig record (src/VindexLLM.Sampler.pas:26-34 under {$A8},
+src/VindexLLM.Defines.inc:13), and fails loudly when no GPU is present."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vdx_sampler.h")
+
+
+def _lib():
+    from vindexllm_amd import build, sampler
+
+    if not os.path.exists(build.LIB):
+        build.build_library()
+    return sampler.load_library()
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vdx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    L = _lib()
+    names = _declared_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(L, n), n
+    # the Python mirror binds exactly the declared set
+    from vindexllm_amd import sampler
+    assert sorted(sampler._SIGNATURES) == names
+
+
+def test_config_layout_matches_pascal_record(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "vdx_sampler.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(vdx_sampler_config),"
+        "offsetof(vdx_sampler_config,temperature),offsetof(vdx_sampler_config,top_k),"
+        "offsetof(vdx_sampler_config,top_p),offsetof(vdx_sampler_config,min_p),"
+        "offsetof(vdx_sampler_config,repeat_penalty),offsetof(vdx_sampler_config,repeat_window),"
+        "offsetof(vdx_sampler_config,seed));return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert [int(x) for x in out] == [32, 0, 4, 8, 12, 16, 20, 24]
+    from vindexllm_amd import TVdxSamplerConfig
+    assert C.sizeof(TVdxSamplerConfig) == 32
+    assert [getattr(TVdxSamplerConfig, f).offset for f, _ in TVdxSamplerConfig._fields_] == \
+        [0, 4, 8, 12, 16, 20, 24]
+
+
+def test_default_config_matches_reference():
+    # TVdxSampler.DefaultConfig (Sampler.pas:100-109); UTest.Sampler.pas:79-86
+    _lib()
+    from vindexllm_amd import TVdxSampler
+    c = TVdxSampler.DefaultConfig()
+    assert (c.Temperature, c.TopK, c.TopP, c.MinP, c.RepeatPenalty, c.RepeatWindow, c.Seed) == \
+        (0.0, 0, 1.0, 0.0, 1.0, 64, 0)
+
+
+def test_version_string():
+    _lib()
+    from vindexllm_amd import version
+    assert "gfx950" in version()
+
+
+def test_create_fails_loudly_without_gpu():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    _lib()
+    from vindexllm_amd import TVdxSampler, VdxSamplerError
+    with pytest.raises(VdxSamplerError) as e:
+        TVdxSampler(0, 4)
+    assert e.value.code == -2 and "device" in str(e.value)
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from vindexllm_amd import build, sampler
+    monkeypatch.setattr(build, "LIB", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(sampler, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        sampler.load_library()

@@ -1,0 +1,8 @@
+"""MI355X (gfx950) token sampler for VindexLLM: a drop-in for TVdxSampler.
+
+The product is libvdxsampler.so (HIP kernels + C ABI, include/vdx_sampler.h);
+``vindexllm_amd.sampler`` mirrors the reference's Pascal interface over it.
+"""
+from .sampler import (ROW_FALLBACK, ROW_FULL, ROW_GREEDY, ROW_NAN, ROW_TOPK_FAST,  # noqa: F401
+                      ROW_TOPK_REPLAY, VDX_RNG_PHILOX, VDX_RNG_XOSHIRO, TVdxSampler,
+                      TVdxSamplerConfig, VdxSamplerError, load_library, version)

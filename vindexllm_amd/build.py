@@ -1,0 +1,52 @@
+"""Builds libvdxsampler.so (HIP, gfx950) in-tree with hipcc.
+
+The library is the product: hand-written HIP kernels plus the C ABI declared
+in include/vdx_sampler.h.  It is built into vindexllm_amd/lib/ so that it
+travels with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIBDIR = os.path.join(PKG, "lib")
+LIB = os.path.join(LIBDIR, "libvdxsampler.so")
+SOURCES = ["vdx_api.hip", "vdx_kernels.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # bit-exact fp32 semantics: no FMA contraction, IEEE denormals,
+    # correctly rounded division (HIP's default)
+    "-ffp-contract=off",
+    "-fno-gpu-flush-denormals-to-zero",
+    # no packed FP32 instructions
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compiles every source for gfx950; always recompiles."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp,
+           *[os.path.join(CSRC, s) for s in SOURCES]]
+    r = subprocess.run(cmd, cwd=CSRC, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + r.stdout + r.stderr)
+    if verbose:
+        print(" ".join(cmd))
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

@@ -1,0 +1,407 @@
+// vdx_api.hip -- C ABI of libvdxsampler.so (declared in include/vdx_sampler.h).
+//
+// Host half of the drop-in for TVdxSampler (src/VindexLLM.Sampler.pas:37-91):
+// configuration, per-row history rings and RNG state in HBM, workspace
+// management, and the launches of the kernels in vdx_kernels.hip.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+
+#include <string>
+
+#include "../../include/vdx_sampler.h"
+#include "vdx_internal.hpp"
+
+using namespace vdx;
+
+struct vdx_sampler {
+  int32_t device = 0;
+  int32_t max_rows = 0;
+  vdx_sampler_config cfg{};
+  int32_t rng_kind = VDX_RNG_XOSHIRO;
+  uint64_t seed_base = 0;  // resolved seed: Seed, or a timer value when Seed = 0
+  bool hist_maybe = false; // some row may hold history ids
+  hipStream_t stream = nullptr;
+  RowState *d_rows = nullptr;
+  int32_t *d_hist = nullptr;
+  int32_t hist_len = 0;
+  // workspace (sized for ws_chunks chunks per row)
+  int32_t ws_chunks = 0;
+  ChunkMeta *d_meta = nullptr;
+  Cand *d_cand = nullptr;
+  FullMeta *d_fmeta = nullptr;
+  uint64_t *d_gpart = nullptr;
+  uint32_t *d_tickets = nullptr;
+  // host-pointer Process
+  float *d_row = nullptr;
+  int32_t row_cap = 0;
+  int32_t *d_tok = nullptr;
+  std::string err;
+};
+
+static std::string g_create_err;
+
+static int fail(vdx_sampler *s, int code, const std::string &msg) {
+  if (s) s->err = msg;
+  return code;
+}
+
+static int hip_fail(vdx_sampler *s, hipError_t e, const char *where) {
+  std::string m = std::string(where) + ": " + hipGetErrorString(e);
+  return fail(s, VDX_E_HIP, m);
+}
+
+#define HIP_TRY(s, expr)                                   \
+  do {                                                     \
+    hipError_t _e = (expr);                                \
+    if (_e != hipSuccess) return hip_fail((s), _e, #expr); \
+  } while (0)
+
+static uint64_t timer_seed() {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
+}
+
+static int32_t chunks_for(int32_t vocab) { return (vocab + kChunk - 1) / kChunk; }
+
+// Reseeds rows [0, max_rows): SeedPRNG (Sampler.pas:224-241) with Seed + row.
+static int reseed_all(vdx_sampler *s) {
+  s->seed_base = (s->cfg.seed == 0) ? timer_seed() : (uint64_t)s->cfg.seed;
+  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, false, true, s->seed_base, s->stream));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  return VDX_OK;
+}
+
+static int alloc_history(vdx_sampler *s, int32_t window) {
+  if (s->d_hist) {
+    (void)hipFree(s->d_hist);
+    s->d_hist = nullptr;
+  }
+  s->hist_len = window > 0 ? window : 0;
+  if (s->hist_len > 0) {
+    const size_t bytes = (size_t)s->max_rows * s->hist_len * sizeof(int32_t);
+    HIP_TRY(s, hipMalloc(&s->d_hist, bytes));
+    HIP_TRY(s, hipMemsetAsync(s->d_hist, 0, bytes, s->stream));
+  }
+  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, true, false, 0, s->stream));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  s->hist_maybe = false;
+  return VDX_OK;
+}
+
+// EnsureWorkspace (Sampler.pas:250-263) for the device path: grows the
+// per-row chunk records when a larger vocabulary is first seen.
+static int ensure_workspace(vdx_sampler *s, int32_t vocab) {
+  const int32_t S = chunks_for(vocab);
+  if (S <= s->ws_chunks) return VDX_OK;
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  (void)hipFree(s->d_meta);
+  (void)hipFree(s->d_cand);
+  (void)hipFree(s->d_fmeta);
+  (void)hipFree(s->d_gpart);
+  s->d_meta = nullptr;
+  s->d_cand = nullptr;
+  s->d_fmeta = nullptr;
+  s->d_gpart = nullptr;
+  s->ws_chunks = 0;
+  const size_t rc = (size_t)s->max_rows * S;
+  HIP_TRY(s, hipMalloc(&s->d_meta, rc * sizeof(ChunkMeta)));
+  HIP_TRY(s, hipMalloc(&s->d_cand, rc * kCandCap * sizeof(Cand)));
+  HIP_TRY(s, hipMalloc(&s->d_fmeta, rc * sizeof(FullMeta)));
+  HIP_TRY(s, hipMalloc(&s->d_gpart, rc * sizeof(uint64_t)));
+  // every record is written by its chunk before the row's last workgroup reads it
+  s->ws_chunks = S;
+  return VDX_OK;
+}
+
+extern "C" {
+
+const char *vdx_sampler_version(void) { return "vdxsampler 0.1.0 (gfx950)"; }
+
+void vdx_sampler_default_config(vdx_sampler_config *c) {
+  if (!c) return;
+  c->temperature = 0.0f;
+  c->top_k = 0;
+  c->top_p = 1.0f;
+  c->min_p = 0.0f;
+  c->repeat_penalty = 1.0f;
+  c->repeat_window = 64;
+  c->seed = 0;
+}
+
+const char *vdx_sampler_last_error(const vdx_sampler *s) {
+  return s ? s->err.c_str() : g_create_err.c_str();
+}
+
+void vdx_sampler_destroy(vdx_sampler *s) {
+  if (!s) return;
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(s->device);
+  if (s->stream) (void)hipStreamSynchronize(s->stream);
+  (void)hipFree(s->d_rows);
+  (void)hipFree(s->d_hist);
+  (void)hipFree(s->d_meta);
+  (void)hipFree(s->d_cand);
+  (void)hipFree(s->d_fmeta);
+  (void)hipFree(s->d_gpart);
+  (void)hipFree(s->d_tickets);
+  (void)hipFree(s->d_row);
+  (void)hipFree(s->d_tok);
+  if (s->stream) (void)hipStreamDestroy(s->stream);
+  (void)hipSetDevice(cur);
+  delete s;
+}
+
+int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows) {
+  if (!out || max_rows <= 0) {
+    g_create_err = "vdx_sampler_create: out must be non-NULL and max_rows > 0";
+    return VDX_E_INVALID_ARG;
+  }
+  *out = nullptr;
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess || device < 0 || device >= ndev) {
+    g_create_err = std::string("vdx_sampler_create: no HIP device ") + std::to_string(device) +
+                   (e != hipSuccess ? std::string(" (") + hipGetErrorString(e) + ")" : "");
+    return VDX_E_HIP;
+  }
+  vdx_sampler *s = new vdx_sampler();
+  s->device = device;
+  s->max_rows = max_rows;
+  vdx_sampler_default_config(&s->cfg);
+  int rc = VDX_OK;
+  do {
+    if ((e = hipSetDevice(device)) != hipSuccess) { rc = hip_fail(s, e, "hipSetDevice"); break; }
+    if ((e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipStreamCreate");
+      break;
+    }
+    if ((e = hipMalloc(&s->d_rows, sizeof(RowState) * max_rows)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMalloc(rows)");
+      break;
+    }
+    if ((e = hipMemset(s->d_rows, 0, sizeof(RowState) * max_rows)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMemset(rows)");
+      break;
+    }
+    if ((e = hipMalloc(&s->d_tickets, sizeof(uint32_t) * max_rows)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMalloc(tickets)");
+      break;
+    }
+    if ((e = hipMemset(s->d_tickets, 0, sizeof(uint32_t) * max_rows)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMemset(tickets)");
+      break;
+    }
+    if ((e = hipMalloc(&s->d_tok, sizeof(int32_t) * 4)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMalloc(tok)");
+      break;
+    }
+    if ((rc = alloc_history(s, s->cfg.repeat_window)) != VDX_OK) break;
+    if ((rc = reseed_all(s)) != VDX_OK) break;  // Create seeds from the timer (Seed = 0)
+    if ((e = hipDeviceSynchronize()) != hipSuccess) { rc = hip_fail(s, e, "hipDeviceSynchronize"); break; }
+  } while (0);
+  if (rc != VDX_OK) {
+    g_create_err = s->err;
+    vdx_sampler_destroy(s);
+    return rc;
+  }
+  *out = s;
+  return VDX_OK;
+}
+
+int vdx_sampler_set_config(vdx_sampler *s, const vdx_sampler_config *c) {
+  if (!s || !c) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  const bool seed_changed = c->seed != s->cfg.seed;
+  s->cfg = *c;
+  const int32_t want = c->repeat_window > 0 ? c->repeat_window : 0;
+  if (want != s->hist_len) {
+    int rc = alloc_history(s, c->repeat_window);
+    if (rc != VDX_OK) return rc;
+  }
+  if (seed_changed) return reseed_all(s);
+  return VDX_OK;
+}
+
+int vdx_sampler_get_config(const vdx_sampler *s, vdx_sampler_config *out) {
+  if (!s || !out) return VDX_E_INVALID_ARG;
+  *out = s->cfg;
+  return VDX_OK;
+}
+
+int vdx_sampler_set_rng(vdx_sampler *s, int32_t kind) {
+  if (!s || (kind != VDX_RNG_XOSHIRO && kind != VDX_RNG_PHILOX)) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  s->rng_kind = kind;
+  return reseed_all(s);
+}
+
+int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int32_t vocab,
+                               int64_t row_stride, const float *uniforms,
+                               const vdx_sample_outputs *out, void *stream) {
+  if (!s) return VDX_E_INVALID_ARG;
+  if (!logits || !out || !out->tokens)
+    return fail(s, VDX_E_INVALID_ARG, "process_device: logits and out->tokens are required");
+  if (rows <= 0 || rows > s->max_rows)
+    return fail(s, VDX_E_INVALID_ARG, "process_device: rows must be in [1, max_rows]");
+  if (vocab <= 0 || row_stride < vocab)
+    return fail(s, VDX_E_INVALID_ARG, "process_device: need vocab > 0 and row_stride >= vocab");
+  const vdx_sampler_config &c = s->cfg;
+  const bool greedy = (c.temperature == 0.0f);
+  const bool topk = !greedy && c.top_k > 0 && c.top_k < vocab;
+  if ((out->topk_idx || out->topk_prob) && topk && out->topk_stride < c.top_k)
+    return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= TopK");
+  if (topk && c.top_k > kKMax)
+    return fail(s, VDX_E_UNSUPPORTED, "process_device: TopK > 64 is not implemented on the GPU");
+  if (chunks_for(vocab) > kMaxChunks)
+    return fail(s, VDX_E_UNSUPPORTED, "process_device: vocab > 4194304 is not supported");
+  HIP_TRY(s, hipSetDevice(s->device));
+  int rc = ensure_workspace(s, vocab);
+  if (rc != VDX_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+
+  CallParams p{};
+  p.logits = logits;
+  p.stride = row_stride;
+  p.rows = rows;
+  p.vocab = vocab;
+  p.nchunks = chunks_for(vocab);
+  p.vec = ((uintptr_t)logits % 16 == 0) && (row_stride % 4 == 0);
+  p.inv_t = greedy ? 0.0f : 1.0f / c.temperature;  // Sampler.pas:325
+  p.top_k = c.top_k;
+  p.top_p = c.top_p;
+  p.min_p = c.min_p;
+  p.penalty = c.repeat_penalty;
+  p.hist = s->d_hist;
+  p.hist_len = s->hist_len;
+  p.rng.uniforms = uniforms;
+  p.rng.rows = s->d_rows;
+  p.rng.kind = s->rng_kind;
+  p.rng.key = s->seed_base;
+  p.rng.u_out = out->uniforms;
+  p.out.tokens = out->tokens;
+  p.out.topk_idx = topk ? out->topk_idx : nullptr;
+  p.out.topk_prob = topk ? out->topk_prob : nullptr;
+  p.out.topk_stride = out->topk_stride;
+  p.out.flags = out->flags;
+  p.meta = s->d_meta;
+  p.cand = s->d_cand;
+  p.fmeta = s->d_fmeta;
+  p.gpart = s->d_gpart;
+  p.tickets = s->d_tickets;
+
+  // Step 0: repetition penalty (Sampler.pas:287)
+  if (c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
+    HIP_TRY(s, launch_penalty(p, st));
+  if (greedy)
+    HIP_TRY(s, launch_greedy(p, st));
+  else if (topk)
+    HIP_TRY(s, launch_topk(p, st));
+  else
+    HIP_TRY(s, launch_full(p, st));
+  return VDX_OK;
+}
+
+int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
+  if (!s) return VDX_E_INVALID_ARG;
+  if (!logits || vocab <= 0) return fail(s, VDX_E_INVALID_ARG, "process: bad logits / vocab");
+  HIP_TRY(s, hipSetDevice(s->device));
+  if (vocab > s->row_cap) {
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+    (void)hipFree(s->d_row);
+    s->d_row = nullptr;
+    s->row_cap = 0;
+    HIP_TRY(s, hipMalloc(&s->d_row, sizeof(float) * (size_t)vocab));
+    s->row_cap = vocab;
+  }
+  HIP_TRY(s, hipMemcpyAsync(s->d_row, logits, sizeof(float) * (size_t)vocab,
+                            hipMemcpyHostToDevice, s->stream));
+  vdx_sample_outputs o{};
+  o.tokens = s->d_tok;
+  int rc = vdx_sampler_process_device(s, s->d_row, 1, vocab, vocab, nullptr, &o, s->stream);
+  if (rc != VDX_OK) return rc;
+  int32_t tok = -1;
+  HIP_TRY(s, hipMemcpyAsync(&tok, s->d_tok, sizeof(int32_t), hipMemcpyDeviceToHost, s->stream));
+  // The reference penalises the caller's buffer in place (Sampler.pas:285-303).
+  if (s->cfg.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
+    HIP_TRY(s, hipMemcpyAsync(logits, s->d_row, sizeof(float) * (size_t)vocab,
+                              hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  return tok;
+}
+
+int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token) {
+  if (!s || row < 0 || row >= s->max_rows) return VDX_E_INVALID_ARG;
+  if (s->cfg.repeat_window <= 0 || s->hist_len <= 0) return VDX_OK;  // Sampler.pas:532-533
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, launch_hist_add(nullptr, token, row, 1, s->d_hist, s->hist_len, s->d_rows, s->stream));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  s->hist_maybe = true;
+  return VDX_OK;
+}
+
+int vdx_sampler_add_to_history_device(vdx_sampler *s, const int32_t *tokens, int32_t rows,
+                                      void *stream) {
+  if (!s || !tokens || rows <= 0 || rows > s->max_rows) return VDX_E_INVALID_ARG;
+  if (s->cfg.repeat_window <= 0 || s->hist_len <= 0) return VDX_OK;
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, launch_hist_add(tokens, 0, 0, rows, s->d_hist, s->hist_len, s->d_rows,
+                             (hipStream_t)stream));
+  s->hist_maybe = true;
+  return VDX_OK;
+}
+
+int vdx_sampler_reset_history(vdx_sampler *s, int32_t row) {
+  if (!s || row >= s->max_rows) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  const int32_t r0 = row < 0 ? 0 : row;
+  const int32_t n = row < 0 ? s->max_rows : 1;
+  // ResetHistory (Sampler.pas:541-549): reseed only when Seed > 0
+  const bool reseed = s->cfg.seed > 0;
+  HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, reseed, s->seed_base, s->stream));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  if (row < 0) s->hist_maybe = false;
+  return VDX_OK;
+}
+
+int vdx_sampler_set_history(vdx_sampler *s, int32_t row, const int32_t *ids, int32_t count,
+                            int32_t pos) {
+  if (!s || row < 0 || row >= s->max_rows || count < 0 || count > s->hist_len ||
+      (count > 0 && !ids) || pos < 0 || (s->hist_len > 0 && pos >= s->hist_len) ||
+      (s->hist_len == 0 && pos != 0))
+    return fail(s, VDX_E_INVALID_ARG, "set_history: need 0 <= count <= window, 0 <= pos < window");
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  if (count > 0)
+    HIP_TRY(s, hipMemcpy(s->d_hist + (int64_t)row * s->hist_len, ids, sizeof(int32_t) * count,
+                         hipMemcpyHostToDevice));
+  RowState rs;
+  HIP_TRY(s, hipMemcpy(&rs, s->d_rows + row, sizeof(RowState), hipMemcpyDeviceToHost));
+  rs.hist_pos = pos;
+  rs.hist_count = count;
+  HIP_TRY(s, hipMemcpy(s->d_rows + row, &rs, sizeof(RowState), hipMemcpyHostToDevice));
+  if (count > 0) s->hist_maybe = true;
+  return VDX_OK;
+}
+
+int32_t vdx_sampler_get_history(vdx_sampler *s, int32_t row, int32_t *ids, int32_t cap,
+                                int32_t *pos) {
+  if (!s || row < 0 || row >= s->max_rows || cap < 0 || (cap > 0 && !ids))
+    return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  RowState rs;
+  HIP_TRY(s, hipMemcpy(&rs, s->d_rows + row, sizeof(RowState), hipMemcpyDeviceToHost));
+  const int32_t n = rs.hist_count < cap ? rs.hist_count : cap;
+  if (n > 0)
+    HIP_TRY(s, hipMemcpy(ids, s->d_hist + (int64_t)row * s->hist_len, sizeof(int32_t) * n,
+                         hipMemcpyDeviceToHost));
+  if (pos) *pos = rs.hist_pos;
+  return rs.hist_count;
+}
+
+}  // extern "C"

@@ -1,0 +1,227 @@
+// vdx_device.hpp -- device-side building blocks of the gfx950 sampler:
+// order-preserving float keys, wave64 reductions and scans, the two RNGs,
+// and the workspace records the kernels exchange through HBM.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vdx {
+
+// ---- launch geometry --------------------------------------------------------
+constexpr int kBlock = 256;                    // threads per workgroup (4 waves)
+constexpr int kWaves = kBlock / 64;
+constexpr int kPerThread = 64;                 // logits per thread per chunk
+constexpr int kChunk = kBlock * kPerThread;    // 16384 logits (64 KiB) per chunk
+constexpr int kWaveSpan = 64 * kPerThread;     // 4096 contiguous logits per wave
+constexpr int kKMax = 64;                      // top-K held one slot per lane
+constexpr int kCandCap = 256;                  // candidates stored per chunk
+constexpr int kMaxChunks = 256;                // V <= 4 Mi logits
+constexpr int kMergeCap = 2048;                // merge-phase LDS candidates
+constexpr int kReplayTile0 = 2048;             // first replay tile (logits)
+constexpr int kReplayTile = 4096;              // later replay tiles (logits)
+constexpr int kReplayCap = 2048;               // replay candidates per batch
+
+// ---- per-row state kept in HBM -------------------------------------------------
+struct RowState {
+  uint64_t rng[4];      // xoshiro256** state (Sampler.pas:41-45)
+  uint64_t step;        // Philox block counter
+  int32_t hist_pos;     // ring write position (Sampler.pas:49)
+  int32_t hist_count;   // ring fill (Sampler.pas:50)
+};
+
+// Top-K stream phase: one record per (row, chunk).
+struct ChunkMeta {
+  uint32_t tau_key;     // every logit of the chunk with key >= tau_key is stored
+  uint32_t count;       // candidates found (may exceed kCandCap: overflow)
+  uint32_t max_key;     // chunk maximum (non-NaN) as a key
+  uint32_t flags;       // bit 0: a non-finite logit was seen
+};
+
+struct Cand {
+  float v;
+  int32_t idx;
+};
+
+// Full-softmax path: one record per (row, chunk).
+struct FullMeta {
+  float m;              // chunk max of s = fl32(L * invT)
+  uint32_t flags;       // bit 0: non-finite s seen
+  double d;             // sum of weights relative to m (or to the row max)
+  double dw[kWaves];    // the same per wave (4096-logit segments)
+};
+
+struct KernelRng {
+  const float *uniforms;  // injected per-row u (nullable)
+  RowState *rows;
+  int32_t kind;           // 0 xoshiro, 1 philox
+  uint64_t key;           // Philox key word 0 (resolved seed)
+  float *u_out;           // optional copy of the consumed u
+};
+
+struct KernelOut {
+  int32_t *tokens;
+  int32_t *topk_idx;
+  float *topk_prob;
+  int32_t topk_stride;
+  uint32_t *flags;
+};
+
+constexpr uint32_t kRowGreedy = 0x1, kRowTopkFast = 0x2, kRowTopkReplay = 0x4,
+                   kRowFull = 0x8, kRowNan = 0x10, kRowFallback = 0x20;
+
+// ---- float keys ------------------------------------------------------------------
+// Order-preserving map of a non-NaN float to uint32 in which -0 and +0 share a
+// key (the reference compares them equal).  -inf -> 0x007FFFFF, +inf ->
+// 0xFF800000; key 0 is below every float and marks "no value".
+__device__ __forceinline__ uint32_t ord_key(float x) {
+  uint32_t b = __float_as_uint(x);
+  b = (b == 0x80000000u) ? 0u : b;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(b);
+}
+// Key used by the reference's min-buffer replay: NaN never becomes the
+// minimum, so it maps above +inf.
+__device__ __forceinline__ uint32_t slot_key(float x) {
+  return (x != x) ? 0xFFFFFFFFu : ord_key(x);
+}
+
+// ---- wave64 primitives --------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor((unsigned long long)v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
+  return v;
+}
+// Inclusive scans (Hillis-Steele over the 64 lanes).
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint32_t w = (uint32_t)__shfl_up((int)v, o);
+    if (l >= o) v += w;
+  }
+  return v;
+}
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    double w = __shfl_up(v, o);
+    if (l >= o) v += w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// ---- RNG -------------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int k) {
+  return (x << k) | (x >> (64 - k));
+}
+// xoshiro256** step (Sampler.pas:208-222); returns the output word.
+__device__ __forceinline__ uint64_t xoshiro_next(uint64_t s[4]) {
+  const uint64_t r = rotl64(s[1] * 5ull, 7) * 9ull;
+  const uint64_t t = s[1] << 17;
+  s[2] ^= s[0];
+  s[3] ^= s[1];
+  s[1] ^= s[2];
+  s[0] ^= s[3];
+  s[2] ^= t;
+  s[3] = rotl64(s[3], 45);
+  return r;
+}
+// Philox4x64-10 (Salmon et al., SC'11), word 0 only.
+__device__ __forceinline__ uint64_t philox4x64_10_w0(uint64_t c0, uint64_t c1,
+                                                     uint64_t c2, uint64_t c3,
+                                                     uint64_t k0, uint64_t k1) {
+  const uint64_t M0 = 0xD2E7470EE14C6C93ull, M1 = 0xCA5A826395121157ull;
+  const uint64_t W0 = 0x9E3779B97F4A7C15ull, W1 = 0xBB67AE8584CAA73Bull;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) {
+      k0 += W0;
+      k1 += W1;
+    }
+    const uint64_t hi0 = __umul64hi(M0, c0), lo0 = M0 * c0;
+    const uint64_t hi1 = __umul64hi(M1, c2), lo1 = M1 * c2;
+    const uint64_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  return c0;
+}
+// (x >> 40) / 2^24 (Sampler.pas:247).
+__device__ __forceinline__ float u24(uint64_t x) {
+  return (float)(x >> 40) * (1.0f / 16777216.0f);
+}
+// One uniform for `row`: injected, or drawn (advancing that row's RNG).
+// Called by exactly one thread per row.
+__device__ __forceinline__ float draw_uniform(const KernelRng &g, int row) {
+  float u;
+  if (g.uniforms) {
+    u = g.uniforms[row];
+  } else if (g.kind == 1) {
+    const uint64_t step = g.rows[row].step;
+    u = u24(philox4x64_10_w0(step, (uint64_t)row, 0, 0, g.key, 0));
+    g.rows[row].step = step + 1;
+  } else {
+    uint64_t s[4] = {g.rows[row].rng[0], g.rows[row].rng[1], g.rows[row].rng[2],
+                     g.rows[row].rng[3]};
+    u = u24(xoshiro_next(s));
+    g.rows[row].rng[0] = s[0];
+    g.rows[row].rng[1] = s[1];
+    g.rows[row].rng[2] = s[2];
+    g.rows[row].rng[3] = s[3];
+  }
+  if (g.u_out) g.u_out[row] = u;
+  return u;
+}
+
+// Maps a workgroup id to (row, chunk) so that the chunks of one row run on
+// one XCD (workgroups are dealt round-robin over the 8 XCDs).
+__device__ __forceinline__ void block_row_chunk(int nchunks, int rows, int &row, int &chunk) {
+  const int bid = blockIdx.x;
+  const int nb = rows * nchunks;
+  int logical = bid;
+  if ((nb & 7) == 0) logical = (bid & 7) * (nb >> 3) + (bid >> 3);
+  row = logical / nchunks;
+  chunk = logical - row * nchunks;
+}
+
+}  // namespace vdx

@@ -1,0 +1,1167 @@
+// vdx_kernels.hip -- gfx950 kernels of the token sampler.
+//
+// The reference runs TVdxSampler.Process (src/VindexLLM.Sampler.pas:265-528)
+// on the host after downloading each logit row.  Here every stage runs on the
+// GPU over rows that stay in HBM:
+//   k_penalty  repetition penalty, once per history occurrence (:285-303)
+//   k_greedy   first index of the maximum (:306-322)
+//   k_topk     top-K select + softmax / Min-P / Top-P / draw (:327-460)
+//   k_full     full-vocabulary softmax + draw, K = 0 or K >= V (:461-527)
+// Rows are split into 16384-logit chunks, one 256-thread workgroup per chunk;
+// the last workgroup of a row (atomic ticket) merges the chunk results and
+// finishes the row, so a sampling call is one kernel launch per stage.
+#include <math.h>
+
+#include "vdx_internal.hpp"
+
+namespace vdx {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= (uint32_t)__shfl_xor((int)v, o);
+  return v;
+}
+
+// Block-wide exclusive scan of one double per thread (kBlock threads).
+__device__ __forceinline__ double block_excl_scan_f64(double x, double *wtot, double &total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const double incl = wave_incl_scan_f64(x);
+  if (lane == 63) wtot[wv] = incl;
+  __syncthreads();
+  double base = 0.0;
+  total = 0.0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wv) base += wtot[w];
+    total += wtot[w];
+  }
+  __syncthreads();
+  return base + (incl - x);
+}
+
+// Loads one chunk: thread (wave wv, lane) owns logits
+//   wv*4096 + j*256 + lane*4 + e,  j < 16, e < 4
+// (each wave reads a contiguous 16 KiB span, 1 KiB per instruction).
+// Positions at or beyond `clen` read as `fill`.
+template <bool VEC>
+__device__ __forceinline__ void load_chunk(const float *__restrict__ base, int clen, int wv,
+                                           int lane, float (&v)[kPerThread], float fill) {
+#pragma unroll
+  for (int j = 0; j < kPerThread / 4; ++j) {
+    const int local = wv * kWaveSpan + j * 256 + lane * 4;
+    if (VEC && local + 4 <= clen) {
+      const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base + local));
+      v[4 * j + 0] = f[0];
+      v[4 * j + 1] = f[1];
+      v[4 * j + 2] = f[2];
+      v[4 * j + 3] = f[3];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * j + e] = (local + e < clen) ? base[local + e] : fill;
+    }
+  }
+}
+__device__ __forceinline__ int chunk_pos(int wv, int lane, int i) {
+  return wv * kWaveSpan + (i >> 2) * 256 + lane * 4 + (i & 3);
+}
+
+// Last-workgroup election for a row: returns true in every thread of the
+// workgroup that finished the row last.  Writes made before the call by any
+// workgroup of the row are visible to the winner after it returns.
+__device__ __forceinline__ bool last_of_row(uint32_t *tickets, int row, int nchunks, int *flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t t = atomicAdd(&tickets[row], 1u);
+    *flag = (t == (uint32_t)(nchunks - 1));
+  }
+  __syncthreads();
+  if (!*flag) return false;
+  __threadfence();
+  if (threadIdx.x == 0) tickets[row] = 0u;  // every other chunk has arrived
+  return true;
+}
+
+// =============================================================================
+// Repetition penalty (Sampler.pas:285-303).  One workgroup per row; the first
+// occurrence of each in-range id applies the reference's sign test and
+// divide / multiply once per occurrence, in order, with IEEE fp32 arithmetic.
+// =============================================================================
+constexpr int kPenStage = 4096;
+
+__global__ __launch_bounds__(kBlock) void k_penalty(float *__restrict__ logits, int64_t stride,
+                                                    int32_t V, const int32_t *__restrict__ hist,
+                                                    int32_t W, const RowState *__restrict__ rs,
+                                                    float pen) {
+  __shared__ int32_t sh[kPenStage];
+  const int row = blockIdx.x;
+  const int cnt = min(rs[row].hist_count, W);
+  if (cnt <= 0) return;
+  const int32_t *h = hist + (int64_t)row * W;
+  float *L = logits + (int64_t)row * stride;
+  const bool staged = cnt <= kPenStage;
+  if (staged) {
+    for (int j = threadIdx.x; j < cnt; j += kBlock) sh[j] = h[j];
+    __syncthreads();
+  }
+  for (int j = threadIdx.x; j < cnt; j += kBlock) {
+    const int id = staged ? sh[j] : h[j];
+    if (id < 0 || id >= V) continue;
+    int k = 0;
+    bool first = true;
+    for (int jj = 0; jj < cnt; ++jj) {
+      const int o = staged ? sh[jj] : h[jj];
+      if (o == id) {
+        if (jj < j) {
+          first = false;
+          break;
+        }
+        ++k;
+      }
+    }
+    if (!first) continue;
+    float x = L[id];
+    for (int r = 0; r < k; ++r) {
+      if (x > 0.0f)
+        x = x / pen;
+      else if (x < 0.0f)
+        x = x * pen;
+    }
+    L[id] = x;
+  }
+}
+
+// =============================================================================
+// Greedy argmax (Sampler.pas:306-322): the reference's strict '>' scan returns
+// the lowest index of the maximum; a NaN at index 0 absorbs the scan (-> 0),
+// NaNs elsewhere are never chosen.  Key = (ordered value << 32) | ~index.
+// =============================================================================
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
+  __shared__ uint64_t s_w[kWaves];
+  __shared__ int s_last;
+  int row, chunk;
+  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, p.vocab - c0);
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, __builtin_nanf(""));
+  float m = v[0];
+#pragma unroll
+  for (int i = 1; i < kPerThread; ++i) m = fmaxf(m, v[i]);  // NaN-ignoring
+  int first = -1;
+#pragma unroll
+  for (int i = kPerThread - 1; i >= 0; --i)
+    if (v[i] == m) first = i;  // this thread's lowest position of its max
+  uint64_t key = 0;
+  if (first >= 0)
+    key = ((uint64_t)ord_key(m) << 32) |
+          (uint32_t)(~(uint32_t)(c0 + chunk_pos(wv, lane, first)));
+  key = wave_max_u64(key);
+  if (lane == 0) s_w[wv] = key;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t k = s_w[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
+    p.gpart[(int64_t)row * p.nchunks + chunk] = k;
+  }
+  if (!last_of_row(p.tickets, row, p.nchunks, &s_last)) return;
+  uint64_t k = 0;
+  for (int c = tid; c < p.nchunks; c += kBlock) {
+    const uint64_t x = p.gpart[(int64_t)row * p.nchunks + c];
+    k = x > k ? x : k;
+  }
+  k = wave_max_u64(k);
+  __syncthreads();
+  if (lane == 0) s_w[wv] = k;
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
+    int32_t tok = k ? (int32_t)(~(uint32_t)k) : 0;
+    if (L[0] != L[0]) tok = 0;
+    p.out.tokens[row] = tok;
+    if (p.out.flags) p.out.flags[row] = kRowGreedy;
+    if (p.rng.u_out) p.rng.u_out[row] = 0.0f;
+  }
+}
+
+// =============================================================================
+// Top-K path (Sampler.pas:327-460).
+//
+// Stream phase (every chunk): each thread keeps 64 logits in registers.  The
+// threshold tau is the largest of 64 sampled thread maxima that at least K
+// thread maxima reach, so >= K logits of the chunk are >= tau and every logit
+// of the chunk's top K is >= tau.  Logits >= tau (about K of them on smooth
+// data) are written as candidates.
+//
+// Merge phase (last workgroup of the row): candidates >= max(tau) of all
+// chunks are gathered into LDS, filtered once more with a sampled threshold,
+// and rank-sorted by (value desc, index asc).  This is the exact top-K set
+// whenever the K-th value is not tied with a logit outside the set.
+//
+// Finish: when Top-P < 1 runs, the reference's draw order is the stable
+// descending sort of q; with pairwise-distinct non-zero q and all non-zero q
+// within 2^22 of the largest (so every fp64 sum is exact in any order) the
+// result does not depend on the min-buffer's slot order and the fast path
+// finishes in one wave.  Otherwise the row replays the reference min-buffer
+// exactly (first strict-minimum slot evicted) and finishes in slot order.
+// =============================================================================
+struct TopkSmem {
+  uint32_t thr[64];
+  uint32_t cnt[kWaves][64];
+  uint32_t wmax[kWaves];
+  uint32_t wflag[kWaves];
+  uint32_t wtot[kWaves];
+  int32_t last;
+  uint32_t ccount[kMaxChunks];
+  uint32_t n, n2;
+  int32_t ntop;
+  uint64_t topkey[kKMax + 1];
+  float uval;
+  int32_t token;
+  uint32_t rowflags;
+  int32_t replay;
+  uint32_t jw[kReplayTile / kBlock][kWaves];
+  uint32_t jwbase[kReplayTile / kBlock][kWaves];
+  uint32_t ntile;
+  uint32_t minkey;
+  int32_t qnan;
+  float wfmax[kWaves];
+  double S;
+  float slot_v[kKMax];
+  int32_t slot_i[kKMax];
+  float q[kKMax];
+  float q_ord[kKMax];
+  int32_t i_ord[kKMax];
+  float v_ord[kKMax];
+  uint64_t sk2[512];
+  union {
+    uint64_t sk[kMergeCap];
+    struct {
+      float v[kReplayCap];
+      int32_t i[kReplayCap];
+    } rc;
+  } buf;
+};
+
+template <bool VEC>
+__device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0, int clen, int K,
+                                            Cand *__restrict__ cand, ChunkMeta *__restrict__ meta,
+                                            TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const bool full = (clen == kChunk);
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+
+  // thread maximum and a non-finite detector (inf*0 and NaN*0 are NaN)
+  float m = -INFINITY, nf = 0.0f;
+  bool hasv = full;
+  if (full) {
+    m = v[0];
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      m = fmaxf(m, v[i]);
+      nf = __builtin_fmaf(v[i], 0.0f, nf);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      if (chunk_pos(wv, lane, i) < clen) {
+        hasv = true;
+        m = fmaxf(m, v[i]);
+        nf = __builtin_fmaf(v[i], 0.0f, nf);
+      }
+    }
+  }
+  const uint32_t mk = hasv ? ord_key(m) : 0u;
+  const uint64_t badw = __ballot(nf != nf);
+  const uint32_t wm = wave_max_u32(mk);
+  if (lane == 0) {
+    sm.wmax[wv] = wm;
+    sm.wflag[wv] = badw != 0ull;
+  }
+  if (wv == 0) sm.thr[lane] = mk;
+  __syncthreads();
+
+  uint32_t tau = 0u;  // 0: store every logit of a short chunk
+  if (clen > kCandCap) {
+    uint32_t mycnt = 0u;
+#pragma unroll 8
+    for (int j = 0; j < 64; ++j) {
+      const uint32_t tj = sm.thr[j];
+      const uint32_t c = (uint32_t)__popcll(__ballot(mk >= tj));
+      mycnt = (lane == j) ? c : mycnt;
+    }
+    sm.cnt[wv][lane] = mycnt;
+    __syncthreads();
+    const uint32_t tot = sm.cnt[0][lane] + sm.cnt[1][lane] + sm.cnt[2][lane] + sm.cnt[3][lane];
+    const uint32_t tk = sm.thr[lane];
+    tau = wave_max_u32((tot >= (uint32_t)K && tk != 0u) ? tk : 0u);
+  }
+  const float tf = key_float(tau);
+
+  // candidate extraction: 4-bit masks per float4 group, then ordered writes
+  uint32_t mlo = 0u, mhi = 0u;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    bool pass;
+    if (full)
+      pass = v[i] >= tf;
+    else
+      pass = (chunk_pos(wv, lane, i) < clen) && (tau == 0u || v[i] >= tf);
+    if (i < 32)
+      mlo |= pass ? (1u << i) : 0u;
+    else
+      mhi |= pass ? (1u << (i - 32)) : 0u;
+  }
+  const uint32_t c = (uint32_t)(__popc(mlo) + __popc(mhi));
+  const uint32_t incl = wave_incl_scan_u32(c);
+  if (lane == 63) sm.wtot[wv] = incl;
+  __syncthreads();
+  uint32_t base = 0u, total = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wv) base += sm.wtot[w];
+    total += sm.wtot[w];
+  }
+  uint32_t pos = base + incl - c;
+  if (c) {
+#pragma unroll
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      const uint32_t g = ((j < 8) ? (mlo >> (4 * j)) : (mhi >> (4 * (j - 8)))) & 0xFu;
+      if (g) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if ((g >> e) & 1u) {
+            if (pos < (uint32_t)kCandCap)
+              cand[pos] = Cand{v[4 * j + e], c0 + chunk_pos(wv, lane, 4 * j + e)};
+            ++pos;
+          }
+        }
+      }
+    }
+  }
+  if (tid == 0) {
+    ChunkMeta cm;
+    cm.tau_key = tau;
+    cm.count = total;
+    cm.max_key = max(max(sm.wmax[0], sm.wmax[1]), max(sm.wmax[2], sm.wmax[3]));
+    cm.flags = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
+    *meta = cm;
+  }
+}
+
+// Merge phase.  Returns false when the row must be replayed (non-finite
+// logits, a chunk overflowed its candidate store, or LDS capacity exceeded).
+__device__ bool topk_merge(int S, int K, const ChunkMeta *__restrict__ cm,
+                           const Cand *__restrict__ cand_row, TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t mt = 0u, fl = 0u, ovf = 0u;
+  for (int c = tid; c < S; c += kBlock) {
+    const ChunkMeta x = cm[c];
+    mt = max(mt, x.tau_key);
+    fl |= x.flags;
+    ovf |= (x.count > (uint32_t)kCandCap) ? 1u : 0u;
+    sm.ccount[c] = min(x.count, (uint32_t)kCandCap);
+  }
+  mt = wave_max_u32(mt);
+  fl = wave_or_u32(fl);
+  ovf = wave_or_u32(ovf);
+  if (lane == 0) {
+    sm.cnt[0][wv] = mt;
+    sm.cnt[1][wv] = fl;
+    sm.cnt[2][wv] = ovf;
+  }
+  if (tid == 0) sm.n = 0u;
+  __syncthreads();
+  mt = max(max(sm.cnt[0][0], sm.cnt[0][1]), max(sm.cnt[0][2], sm.cnt[0][3]));
+  fl = sm.cnt[1][0] | sm.cnt[1][1] | sm.cnt[1][2] | sm.cnt[1][3];
+  ovf = sm.cnt[2][0] | sm.cnt[2][1] | sm.cnt[2][2] | sm.cnt[2][3];
+  __syncthreads();
+  if (fl || ovf) return false;
+
+  // gather candidates >= max tau: kBlock/S threads per chunk
+  const int tpc = kBlock / S;
+  const int c = tid / tpc, sub = tid - c * tpc;
+  if (c < S) {
+    const uint32_t nc = sm.ccount[c];
+    for (uint32_t e = (uint32_t)sub; e < nc; e += (uint32_t)tpc) {
+      const Cand x = cand_row[(int64_t)c * kCandCap + e];
+      const uint32_t k = ord_key(x.v);
+      if (k >= mt) {
+        const uint32_t p = atomicAdd(&sm.n, 1u);
+        if (p < (uint32_t)kMergeCap) sm.buf.sk[p] = ((uint64_t)k << 32) | (uint32_t)(~(uint32_t)x.idx);
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t n = sm.n;
+  if (n > (uint32_t)kMergeCap) return false;
+
+  const uint64_t *src = sm.buf.sk;
+  uint32_t n2 = n;
+  if (n > 128u) {
+    // second sampled threshold over the gathered keys
+    if (wv == 0) sm.thr[lane] = (uint32_t)(sm.buf.sk[lane] >> 32);
+    if (tid == 0) sm.n2 = 0u;
+    __syncthreads();
+    const int nr = (int)((n + kBlock - 1) / kBlock);
+    uint32_t mycnt = 0u;
+    for (int r = 0; r < nr; ++r) {
+      const uint32_t i = (uint32_t)(tid + r * kBlock);
+      const uint32_t key = (i < n) ? (uint32_t)(sm.buf.sk[i] >> 32) : 0u;
+      for (int j = 0; j < 64; ++j) {
+        const uint32_t cj = (uint32_t)__popcll(__ballot(key >= sm.thr[j]));
+        mycnt += (lane == j) ? cj : 0u;
+      }
+    }
+    sm.cnt[wv][lane] = mycnt;
+    __syncthreads();
+    const uint32_t tot = sm.cnt[0][lane] + sm.cnt[1][lane] + sm.cnt[2][lane] + sm.cnt[3][lane];
+    const uint32_t t2 = wave_max_u32(tot >= (uint32_t)K ? sm.thr[lane] : 0u);
+    for (int r = 0; r < nr; ++r) {
+      const uint32_t i = (uint32_t)(tid + r * kBlock);
+      if (i < n) {
+        const uint64_t k = sm.buf.sk[i];
+        if ((uint32_t)(k >> 32) >= t2) {
+          const uint32_t q = atomicAdd(&sm.n2, 1u);
+          if (q < 512u) sm.sk2[q] = k;
+        }
+      }
+    }
+    __syncthreads();
+    n2 = sm.n2;
+    src = sm.sk2;
+    if (n2 > 512u) return false;
+  }
+  // rank sort by (value desc, index asc); keys are unique
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t i = (uint32_t)(tid + r * kBlock);
+    if (i < n2) {
+      const uint64_t key = src[i];
+      uint32_t rank = 0u;
+      for (uint32_t j = 0; j < n2; ++j) rank += (src[j] > key) ? 1u : 0u;
+      if (rank <= (uint32_t)K) sm.topkey[rank] = key;
+    }
+  }
+  if (tid == 0) sm.ntop = (int32_t)min(n2, (uint32_t)(K + 1));
+  __syncthreads();
+  return true;
+}
+
+// Fast finish over the sorted top-K (wave 0).  Sets sm.replay when the
+// exactness conditions do not hold.
+__device__ void topk_fast(const CallParams &p, int row, TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int K = p.top_k;
+  if (tid < 64) {
+    bool elig = (p.top_p < 1.0f) && (p.inv_t > 0.0f) && (p.inv_t <= 3.4028235e38f) && (sm.ntop >= K);
+    if (sm.ntop > K && (uint32_t)(sm.topkey[K] >> 32) == (uint32_t)(sm.topkey[K - 1] >> 32))
+      elig = false;  // the K-th value is tied outside the set
+    const bool act = lane < K;
+    const uint64_t sk = act ? sm.topkey[lane] : 0ull;
+    const float val = key_float((uint32_t)(sk >> 32));
+    const int32_t idx = (int32_t)(~(uint32_t)sk);
+    const float M = key_float((uint32_t)(sm.topkey[0] >> 32));
+    float q = 0.0f;
+    if (act) q = (float)exp(((double)val - (double)M) * (double)p.inv_t);
+    const float qmax = __shfl(q, 0);
+    const float qfloor = ldexpf(qmax, -22);
+    bool bad = act && !(q == 0.0f || (q <= 3.4028235e38f && q >= qfloor));
+    const float qn = __shfl_down(q, 1);
+    bad = bad || ((lane + 1 < K) && qn != 0.0f && qn == q);
+    if (p.min_p > 0.0f) {
+      const float thr = qmax * p.min_p;
+      if (q < thr) q = 0.0f;
+    }
+    const double s1 = wave_sum_f64((double)q);
+    const double target = (double)p.top_p * s1;
+    const double incl = wave_incl_scan_f64((double)q);
+    const double excl = incl - (double)q;
+    const float qk = (excl < target && q > 0.0f) ? q : 0.0f;
+    const double s2 = wave_sum_f64((double)qk);
+    elig = elig && (__ballot(bad) == 0ull) && (s2 > 0.0);
+    if (elig) {
+      const double t = (double)sm.uval * s2;
+      const double c2 = wave_incl_scan_f64((double)qk);
+      const uint64_t hit = __ballot(act && c2 > t);
+      const int first = hit ? (__ffsll((unsigned long long)hit) - 1) : (K - 1);
+      const int32_t tok = __shfl(idx, first);
+      if (lane == 0) {
+        sm.token = tok;
+        sm.rowflags = kRowTopkFast | (hit ? 0u : kRowFallback);
+        sm.replay = 0;
+      }
+      if (act) {
+        const int64_t o = (int64_t)row * p.out.topk_stride + lane;
+        if (p.out.topk_idx) p.out.topk_idx[o] = idx;
+        if (p.out.topk_prob) p.out.topk_prob[o] = (float)((double)qk / s2);
+      }
+    } else if (lane == 0) {
+      sm.replay = 1;
+    }
+  }
+  __syncthreads();
+}
+
+// Exact replay of the reference min-buffer (Sampler.pas:341-383) and the
+// slot-order finish (:385-459).  Whole workgroup.
+__device__ void topk_replay(const CallParams &p, int row, TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int K = p.top_k, V = p.vocab;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  constexpr int kJ = kReplayTile / kBlock;
+
+  // fill: slots 0..K-1 hold logits 0..K-1 (wave 0, one slot per lane)
+  float sv = 0.0f;
+  int32_t si = -1;
+  uint32_t skey = 0xFFFFFFFFu, mkey = 0xFFFFFFFFu;
+  int mi = 0;
+  float tmax = -INFINITY;
+  const bool frozen = (L[0] != L[0]);  // NaN in slot 0: nothing ever enters
+  if (wv == 0) {
+    if (lane < K) {
+      sv = L[lane];
+      si = lane;
+      skey = slot_key(sv);
+      tmax = fmaxf(tmax, sv);
+    }
+    if (!frozen) {
+      mkey = wave_min_u32(lane < K ? skey : 0xFFFFFFFFu);
+      mi = __ffsll((unsigned long long)__ballot(lane < K && skey == mkey)) - 1;
+    }
+    if (lane == 0) sm.minkey = mkey;
+  }
+  __syncthreads();
+
+  if (!frozen) {
+    int t0 = K;
+    int tend = min(V, kReplayTile0);
+    while (t0 < V) {
+      const int tl = tend - t0;
+      const uint32_t thr = sm.minkey;
+      float v[kJ];
+      uint32_t pm = 0u;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int e = j * kBlock + tid;
+        v[j] = (e < tl) ? L[t0 + e] : __builtin_nanf("");
+      }
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        tmax = fmaxf(tmax, v[j]);
+        const bool pass = (v[j] == v[j]) && (ord_key(v[j]) > thr);
+        pm |= pass ? (1u << j) : 0u;
+        const uint64_t b = __ballot(pass);
+        if (lane == 0) sm.jw[j][wv] = (uint32_t)__popcll(b);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t acc = 0u;
+        for (int j = 0; j < kJ; ++j)
+          for (int w = 0; w < kWaves; ++w) {
+            sm.jwbase[j][w] = acc;
+            acc += sm.jw[j][w];
+          }
+        sm.ntile = acc;
+      }
+      __syncthreads();
+      const uint32_t nt = sm.ntile;
+      for (uint32_t b0 = 0u; b0 < nt; b0 += (uint32_t)kReplayCap) {
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+          const bool pj = (pm >> j) & 1u;
+          const uint64_t b = __ballot(pj);
+          if (pj) {
+            const uint32_t pos = sm.jwbase[j][wv] + (uint32_t)__popcll(b & lanemask_lt());
+            if (pos >= b0 && pos < b0 + (uint32_t)kReplayCap) {
+              sm.buf.rc.v[pos - b0] = v[j];
+              sm.buf.rc.i[pos - b0] = t0 + j * kBlock + tid;
+            }
+          }
+        }
+        __syncthreads();
+        if (wv == 0) {
+          const uint32_t nb = min(nt - b0, (uint32_t)kReplayCap);
+          for (uint32_t g = 0u; g < nb; g += 64u) {
+            const bool has = g + (uint32_t)lane < nb;
+            const float cv = has ? sm.buf.rc.v[g + lane] : 0.0f;
+            const int32_t ci = has ? sm.buf.rc.i[g + lane] : 0;
+            const uint32_t ck = has ? ord_key(cv) : 0u;
+            uint64_t pend = __ballot(has && ck > mkey);
+            while (pend) {
+              const int src = __ffsll((unsigned long long)pend) - 1;
+              const uint32_t ek = (uint32_t)__shfl((int)ck, src);
+              const float ev = __shfl(cv, src);
+              const int32_t ei = __shfl(ci, src);
+              if (lane == mi) {
+                skey = ek;
+                sv = ev;
+                si = ei;
+              }
+              mkey = wave_min_u32(lane < K ? skey : 0xFFFFFFFFu);
+              mi = __ffsll((unsigned long long)__ballot(lane < K && skey == mkey)) - 1;
+              pend &= ~(1ull << src);
+              pend &= __ballot(ck > mkey);
+            }
+          }
+          if (lane == 0) sm.minkey = mkey;
+        }
+        __syncthreads();
+      }
+      t0 = tend;
+      tend = min(V, t0 + kReplayTile);
+    }
+  }
+  // running maximum M (strict '>' from L[0]: NaN at 0 sticks, later NaN skipped)
+  const float wm = wave_max_f32(tmax);
+  if (lane == 0) sm.wfmax[wv] = wm;
+  if (wv == 0 && lane < K) {
+    sm.slot_v[lane] = sv;
+    sm.slot_i[lane] = si;
+  }
+  __syncthreads();
+  const float M = frozen ? __builtin_nanf("")
+                         : fmaxf(fmaxf(sm.wfmax[0], sm.wfmax[1]), fmaxf(sm.wfmax[2], sm.wfmax[3]));
+
+  // softmax over the slots (:385-391)
+  if (wv == 0) {
+    float q = 0.0f;
+    if (lane < K) {
+      q = (float)exp(((double)sm.slot_v[lane] - (double)M) * (double)p.inv_t);
+      sm.q[lane] = q;
+    }
+    const uint64_t nanm = __ballot(lane < K && q != q);
+    if (lane == 0) sm.qnan = nanm != 0ull;
+  }
+  __syncthreads();
+  // sums and Min-P in slot order (:386-410)
+  if (tid == 0) {
+    double S = 0.0;
+    for (int k = 0; k < K; ++k) S = S + (double)sm.q[k];
+    if (p.min_p > 0.0f) {
+      float best = sm.q[0];
+      for (int k = 1; k < K; ++k)
+        if (sm.q[k] > best) best = sm.q[k];
+      const float thr = best * p.min_p;
+      S = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (sm.q[k] < thr)
+          sm.q[k] = 0.0f;
+        else
+          S = S + (double)sm.q[k];
+      }
+    }
+    sm.S = S;
+  }
+  __syncthreads();
+  // draw order: stable descending sort when Top-P runs (:412-429)
+  if (p.top_p < 1.0f) {
+    if (!sm.qnan) {
+      if (wv == 0 && lane < K) {
+        const float qk = sm.q[lane];
+        int rank = 0;
+        for (int j = 0; j < K; ++j) {
+          const float qj = sm.q[j];
+          rank += (qj > qk || (qj == qk && j < lane)) ? 1 : 0;
+        }
+        sm.q_ord[rank] = qk;
+        sm.i_ord[rank] = sm.slot_i[lane];
+        sm.v_ord[rank] = sm.slot_v[lane];
+      }
+    } else if (tid == 0) {
+      for (int k = 0; k < K; ++k) {
+        sm.q_ord[k] = sm.q[k];
+        sm.i_ord[k] = sm.slot_i[k];
+        sm.v_ord[k] = sm.slot_v[k];
+      }
+      for (int i = 1; i < K; ++i) {  // the reference's insertion sort, literally
+        const float qv = sm.q_ord[i];
+        const int32_t ti = sm.i_ord[i];
+        const float tv = sm.v_ord[i];
+        int j = i - 1;
+        while (j >= 0 && sm.q_ord[j] < qv) {
+          sm.q_ord[j + 1] = sm.q_ord[j];
+          sm.i_ord[j + 1] = sm.i_ord[j];
+          sm.v_ord[j + 1] = sm.v_ord[j];
+          --j;
+        }
+        sm.q_ord[j + 1] = qv;
+        sm.i_ord[j + 1] = ti;
+        sm.v_ord[j + 1] = tv;
+      }
+    }
+  } else if (wv == 0 && lane < K) {
+    sm.q_ord[lane] = sm.q[lane];
+    sm.i_ord[lane] = sm.slot_i[lane];
+    sm.v_ord[lane] = sm.slot_v[lane];
+  }
+  __syncthreads();
+  // Top-P cut (:431-444) and draw (:447-459)
+  if (tid == 0) {
+    double S = sm.S;
+    if (p.top_p < 1.0f) {
+      const double target = (double)p.top_p * S;
+      double C = 0.0;
+      S = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (C < target && sm.q_ord[k] > 0.0f) {
+          C = C + (double)sm.q_ord[k];
+          S = S + (double)sm.q_ord[k];
+        } else {
+          sm.q_ord[k] = 0.0f;
+        }
+      }
+    }
+    const double t = (double)sm.uval * S;
+    double C = 0.0;
+    int32_t tok = sm.i_ord[K - 1];
+    uint32_t fl = kRowTopkReplay | kRowFallback;
+    for (int k = 0; k < K; ++k) {
+      C = C + (double)sm.q_ord[k];
+      if (C > t) {
+        tok = sm.i_ord[k];
+        fl = kRowTopkReplay;
+        break;
+      }
+    }
+    if (sm.qnan || !(M == M)) fl |= kRowNan;
+    sm.token = tok;
+    sm.rowflags = fl;
+    sm.S = S;
+  }
+  __syncthreads();
+  if (wv == 0 && lane < K && (p.out.topk_idx || p.out.topk_prob)) {
+    const uint32_t kk = slot_key(sm.v_ord[lane]);
+    const int32_t ii = sm.i_ord[lane];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) {
+      const uint32_t kj = slot_key(sm.v_ord[j]);
+      const int32_t ij = sm.i_ord[j];
+      rank += (kj > kk || (kj == kk && ij < ii)) ? 1 : 0;
+    }
+    const int64_t o = (int64_t)row * p.out.topk_stride + rank;
+    if (p.out.topk_idx) p.out.topk_idx[o] = ii;
+    if (p.out.topk_prob)
+      p.out.topk_prob[o] = (sm.S > 0.0) ? (float)((double)sm.q_ord[lane] / sm.S) : 0.0f;
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_body(const CallParams &p) {
+  __shared__ TopkSmem sm;
+  int row, chunk;
+  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  const int S = p.nchunks, K = p.top_k;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, p.vocab - c0);
+  ChunkMeta *cm = p.meta + (int64_t)row * S;
+  Cand *cr = p.cand + (int64_t)row * S * kCandCap;
+  topk_stream<VEC>(L, c0, clen, K, cr + (int64_t)chunk * kCandCap, cm + chunk, sm);
+  if (!last_of_row(p.tickets, row, S, &sm.last)) return;
+  if (threadIdx.x == 0) {
+    sm.uval = draw_uniform(p.rng, row);
+    sm.replay = 1;
+  }
+  __syncthreads();
+  if (topk_merge(S, K, cm, cr, sm)) topk_fast(p, row, sm);
+  if (sm.replay) topk_replay(p, row, sm);
+  if (threadIdx.x == 0) {
+    p.out.tokens[row] = sm.token;
+    if (p.out.flags) p.out.flags[row] = sm.rowflags;
+  }
+}
+
+// 16-byte aligned rows: four workgroups per CU (<= 128 VGPRs, no spills).
+__global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_body<false>(p); }
+
+// =============================================================================
+// Full-softmax path (Sampler.pas:461-527): s = fl32(L*invT), M = max s,
+// q = fl32(exp(s - M)), S = sum q, first index whose running sum exceeds
+// u*S (index order); any NaN (or +inf, or an all -inf row) makes S NaN and
+// the reference falls back to V-1.  TopP is not applied here (:461-527).
+//
+// Single pass (Min-P off): each chunk reduces its weights exp(s - m_c)
+// relative to its own maximum m_c, per 4096-logit wave segment; the last
+// workgroup rescales by exp(m_c - M), finds the target chunk and segment,
+// and rescans that one segment.  With Min-P on, k_full_max first finds M and
+// the weights are the reference's q with q < MinP zeroed (Qmax = 1).
+// =============================================================================
+struct FullSmem {
+  float wm[kWaves];
+  uint32_t wf[kWaves];
+  double wd[kWaves];
+  double wtot[kWaves];
+  int32_t last;
+  float M;
+  uint32_t bad;
+  float u;
+  int32_t cstar;
+  int32_t hit;
+  int32_t lastnz;
+  double scale;
+  double base;
+  double cincl[kMaxChunks];
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_full_max(CallParams p) {
+  __shared__ float s_m[kWaves];
+  __shared__ uint32_t s_f[kWaves];
+  int row, chunk;
+  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, p.vocab - c0);
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  float m = -INFINITY;
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    if (chunk_pos(wv, lane, i) < clen) {
+      const float s = v[i] * p.inv_t;
+      m = fmaxf(m, s);
+      bad = bad || (s != s);
+    }
+  }
+  m = wave_max_f32(m);
+  const uint64_t b = __ballot(bad);
+  if (lane == 0) {
+    s_m[wv] = m;
+    s_f[wv] = b != 0ull;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    FullMeta *fm = p.fmeta + (int64_t)row * p.nchunks + chunk;
+    fm->m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    fm->flags = s_f[0] | s_f[1] | s_f[2] | s_f[3];
+  }
+}
+
+template <bool VEC, bool EXACT>
+__global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
+  __shared__ FullSmem sm;
+  int row, chunk;
+  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int S = p.nchunks, V = p.vocab;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  FullMeta *fm = p.fmeta + (int64_t)row * S;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, V - c0);
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+
+  // s = fl32(L * invT); positions past the row end weigh nothing
+  float m = -INFINITY;
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    if (chunk_pos(wv, lane, i) < clen) {
+      v[i] = v[i] * p.inv_t;
+      m = fmaxf(m, v[i]);
+      bad = bad || (v[i] != v[i]);
+    } else {
+      v[i] = -INFINITY;
+    }
+  }
+  float base;
+  if (EXACT) {
+    // row maximum from the k_full_max records of this row
+    float mm = -INFINITY;
+    for (int c = tid; c < S; c += kBlock) mm = fmaxf(mm, fm[c].m);
+    mm = wave_max_f32(mm);
+    if (lane == 0) sm.wm[wv] = mm;
+    __syncthreads();
+    base = fmaxf(fmaxf(sm.wm[0], sm.wm[1]), fmaxf(sm.wm[2], sm.wm[3]));
+  } else {
+    m = wave_max_f32(m);
+    const uint64_t b = __ballot(bad);
+    if (lane == 0) {
+      sm.wm[wv] = m;
+      sm.wf[wv] = b != 0ull;
+    }
+    __syncthreads();
+    base = fmaxf(fmaxf(sm.wm[0], sm.wm[1]), fmaxf(sm.wm[2], sm.wm[3]));
+  }
+  double acc = 0.0;
+  if (base > -INFINITY && base < INFINITY) {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      float w;
+      if (EXACT) {
+        const float q = (float)exp((double)v[i] - (double)base);
+        w = (q < p.min_p) ? 0.0f : q;
+      } else {
+        w = expf(v[i] - base);
+      }
+      acc += (double)w;
+    }
+  }
+  const double ws = wave_sum_f64(acc);
+  if (lane == 0) sm.wd[wv] = ws;
+  __syncthreads();
+  if (tid == 0) {
+    FullMeta *me = fm + chunk;
+    double d = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      me->dw[w] = sm.wd[w];
+      d = d + sm.wd[w];
+    }
+    me->d = d;
+    if (!EXACT) {
+      me->m = base;
+      me->flags = sm.wf[0] | sm.wf[1] | sm.wf[2] | sm.wf[3];
+    }
+  }
+  if (!last_of_row(p.tickets, row, S, &sm.last)) return;
+
+  // ---- finish (last workgroup of the row) ----
+  if (tid == 0) sm.u = draw_uniform(p.rng, row);
+  float mc = -INFINITY;
+  uint32_t fl = 0u;
+  double dc = 0.0;
+  if (tid < S) {
+    mc = fm[tid].m;
+    fl = fm[tid].flags;
+    dc = fm[tid].d;
+  }
+  const float wmx = wave_max_f32(mc);
+  const uint32_t wfl = wave_or_u32(fl);
+  __syncthreads();
+  if (lane == 0) {
+    sm.wm[wv] = wmx;
+    sm.wf[wv] = wfl;
+  }
+  __syncthreads();
+  const float M = EXACT ? base : fmaxf(fmaxf(sm.wm[0], sm.wm[1]), fmaxf(sm.wm[2], sm.wm[3]));
+  const bool rowbad = (sm.wf[0] | sm.wf[1] | sm.wf[2] | sm.wf[3]) || !(M > -INFINITY && M < INFINITY);
+  if (rowbad) {
+    if (tid == 0) {
+      p.out.tokens[row] = V - 1;
+      if (p.out.flags) p.out.flags[row] = kRowFull | kRowNan | kRowFallback;
+    }
+    return;
+  }
+  // chunk weights and their running sum in chunk order
+  double wc = 0.0;
+  if (tid < S) wc = EXACT ? dc : dc * exp((double)mc - (double)M);
+  double total;
+  const double excl = block_excl_scan_f64(wc, sm.wtot, total);
+  const double incl = excl + wc;
+  if (tid < S) sm.cincl[tid] = incl;
+  if (tid == 0) {
+    sm.cstar = 0x7FFFFFFF;
+    sm.hit = 0x7FFFFFFF;
+    sm.lastnz = -1;
+  }
+  __syncthreads();
+  const double t = (double)sm.u * total;
+  {
+    const uint64_t h = __ballot(tid < S && incl > t);
+    if (h && lane == __ffsll((unsigned long long)h) - 1) atomicMin(&sm.cstar, (int)tid);
+  }
+  __syncthreads();
+  int cs = (sm.cstar != 0x7FFFFFFF) ? sm.cstar : -1;  // first chunk whose running sum exceeds t
+  if (cs < 0) {
+    // rounding put t at or past the total: take the last chunk that weighs
+    for (int c = S - 1; c >= 0; --c)
+      if (sm.cincl[c] > (c ? sm.cincl[c - 1] : 0.0)) {
+        cs = c;
+        break;
+      }
+    if (cs < 0) cs = S - 1;
+  }
+  // segment of the target chunk (4096-logit wave spans), sequentially
+  const FullMeta tc = fm[cs];
+  const double scale = EXACT ? 1.0 : exp((double)tc.m - (double)M);
+  double before = cs ? sm.cincl[cs - 1] : 0.0;
+  int ws_ = -1;
+  for (int w = 0; w < kWaves; ++w) {
+    const double ww = tc.dw[w] * scale;
+    if (before + ww > t) {
+      ws_ = w;
+      break;
+    }
+    before = before + ww;
+  }
+  if (ws_ < 0) {
+    ws_ = kWaves - 1;
+    before = cs ? sm.cincl[cs - 1] : 0.0;
+    for (int w = 0; w < kWaves - 1; ++w) before = before + tc.dw[w] * scale;
+    while (ws_ > 0 && tc.dw[ws_] == 0.0) {
+      --ws_;
+      before = before - tc.dw[ws_] * scale;
+    }
+  }
+  // rescan that segment: thread tid owns 16 consecutive logits
+  const int seg0 = cs * kChunk + ws_ * kWaveSpan;
+  const int e0 = seg0 + tid * 16;
+  float w16[16];
+  double tsum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = e0 + i;
+    float w = 0.0f;
+    if (e < V) {
+      const float s = L[e] * p.inv_t;
+      if (EXACT) {
+        const float q = (float)exp((double)s - (double)M);
+        w = (q < p.min_p) ? 0.0f : q;
+      } else {
+        w = expf(s - tc.m);
+      }
+    }
+    w16[i] = w;
+    tsum += (double)w;
+  }
+  double segtot;
+  const double tb = block_excl_scan_f64(tsum * scale, sm.wtot, segtot);
+  double run = before + tb;
+  int hit = -1, lastnz = -1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const double w = (double)w16[i] * scale;
+    if (w16[i] > 0.0f) lastnz = e0 + i;
+    run = run + w;
+    if (hit < 0 && w16[i] > 0.0f && run > t) hit = e0 + i;
+  }
+  if (hit >= 0) atomicMin(&sm.hit, hit);
+  if (lastnz >= 0) atomicMax(&sm.lastnz, lastnz);
+  __syncthreads();
+  if (tid == 0) {
+    int32_t tok;
+    uint32_t fl2 = kRowFull;
+    if (sm.hit != 0x7FFFFFFF)
+      tok = sm.hit;
+    else if (sm.lastnz >= 0)
+      tok = sm.lastnz;
+    else {
+      tok = V - 1;
+      fl2 |= kRowFallback;
+    }
+    p.out.tokens[row] = tok;
+    if (p.out.flags) p.out.flags[row] = fl2;
+  }
+}
+
+// =============================================================================
+// History ring (Sampler.pas:530-549) and RNG seeding (Sampler.pas:194-241).
+// =============================================================================
+__global__ void k_hist_add(const int32_t *__restrict__ tokens, int32_t tok_const, int32_t row0,
+                           int32_t rows, int32_t *__restrict__ hist, int32_t W,
+                           RowState *__restrict__ rs) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows || W <= 0) return;
+  const int row = row0 + r;
+  const int32_t tok = tokens ? tokens[r] : tok_const;
+  RowState &s = rs[row];
+  hist[(int64_t)row * W + s.hist_pos] = tok;
+  s.hist_pos = (s.hist_pos + 1) % W;
+  if (s.hist_count < W) s.hist_count = s.hist_count + 1;
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t &s) {
+  s += 0x9E3779B97F4A7C15ull;
+  uint64_t z = s;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t rows, int clear_hist,
+                            int reseed, uint64_t seed_base) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int row = row0 + r;
+  RowState &s = rs[row];
+  if (clear_hist) {
+    s.hist_pos = 0;
+    s.hist_count = 0;
+  }
+  if (reseed) {
+    uint64_t st = seed_base + (uint64_t)row;  // row r behaves as a sampler with Seed + r
+    s.rng[0] = splitmix64(st);
+    s.rng[1] = splitmix64(st);
+    s.rng[2] = splitmix64(st);
+    s.rng[3] = splitmix64(st);
+    s.step = 0;
+  }
+}
+
+// =============================================================================
+// Host launchers
+// =============================================================================
+static inline dim3 grid_rows_chunks(const CallParams &p) {
+  return dim3((unsigned)(p.rows * p.nchunks));
+}
+
+hipError_t launch_penalty(const CallParams &p, hipStream_t st) {
+  hipLaunchKernelGGL(k_penalty, dim3(p.rows), dim3(kBlock), 0, st, p.logits, p.stride, p.vocab,
+                     p.hist, p.hist_len, (const RowState *)p.rng.rows, p.penalty);
+  return hipGetLastError();
+}
+
+hipError_t launch_greedy(const CallParams &p, hipStream_t st) {
+  if (p.vec)
+    hipLaunchKernelGGL(k_greedy<true>, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  else
+    hipLaunchKernelGGL(k_greedy<false>, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const CallParams &p, hipStream_t st) {
+  if (p.vec)
+    hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  else
+    hipLaunchKernelGGL(k_topk_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_full(const CallParams &p, hipStream_t st) {
+  const dim3 g = grid_rows_chunks(p);
+  if (p.min_p > 0.0f) {
+    if (p.vec) {
+      hipLaunchKernelGGL(k_full_max<true>, g, dim3(kBlock), 0, st, p);
+      hipLaunchKernelGGL((k_full<true, true>), g, dim3(kBlock), 0, st, p);
+    } else {
+      hipLaunchKernelGGL(k_full_max<false>, g, dim3(kBlock), 0, st, p);
+      hipLaunchKernelGGL((k_full<false, true>), g, dim3(kBlock), 0, st, p);
+    }
+  } else {
+    if (p.vec)
+      hipLaunchKernelGGL((k_full<true, false>), g, dim3(kBlock), 0, st, p);
+    else
+      hipLaunchKernelGGL((k_full<false, false>), g, dim3(kBlock), 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row0, int32_t rows,
+                           int32_t *hist, int32_t hist_len, RowState *rs, hipStream_t st) {
+  const int nb = (rows + 255) / 256;
+  hipLaunchKernelGGL(k_hist_add, dim3(nb), dim3(256), 0, st, tokens, tok_const, row0, rows, hist,
+                     hist_len, rs);
+  return hipGetLastError();
+}
+
+hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, bool reseed,
+                            uint64_t seed_base, hipStream_t st) {
+  const int nb = (rows + 255) / 256;
+  hipLaunchKernelGGL(k_row_reset, dim3(nb), dim3(256), 0, st, rs, row0, rows, clear_hist ? 1 : 0,
+                     reseed ? 1 : 0, seed_base);
+  return hipGetLastError();
+}
+
+}  // namespace vdx

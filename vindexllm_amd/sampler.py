@@ -1,0 +1,274 @@
+"""Python mirror of the reference sampler interface over libvdxsampler.so.
+
+``TVdxSamplerConfig`` and ``TVdxSampler`` keep the names, argument meaning
+and defaults of src/VindexLLM.Sampler.pas:26-91 (Create / SetConfig /
+GetConfig / DefaultConfig / Process / AddToHistory / ResetHistory).  Every
+call goes through the C ABI of include/vdx_sampler.h; sampling runs in the
+library's HIP kernels on the GPU.  There is no CPU fallback: if the library
+is not built, or no GPU is present, construction raises.
+
+Beyond the reference (whose sampler holds one sequence), ``process_device``
+samples a batch of device-resident rows (torch tensors on the GPU) without
+moving logits to the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from . import build as _build
+
+VDX_OK = 0
+VDX_E_INVALID_ARG = -1
+VDX_E_HIP = -2
+VDX_E_UNSUPPORTED = -3
+VDX_E_NO_MEMORY = -4
+
+VDX_RNG_XOSHIRO = 0
+VDX_RNG_PHILOX = 1
+
+ROW_GREEDY = 0x1
+ROW_TOPK_FAST = 0x2
+ROW_TOPK_REPLAY = 0x4
+ROW_FULL = 0x8
+ROW_NAN = 0x10
+ROW_FALLBACK = 0x20
+
+
+class VdxSamplerError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"vdx_sampler error {code}: {msg}")
+        self.code = code
+
+
+class TVdxSamplerConfig(C.Structure):
+    """TVdxSamplerConfig (Sampler.pas:26-34); 32 bytes like the {$A8} record."""
+
+    _fields_ = [
+        ("Temperature", C.c_float),
+        ("TopK", C.c_int32),
+        ("TopP", C.c_float),
+        ("MinP", C.c_float),
+        ("RepeatPenalty", C.c_float),
+        ("RepeatWindow", C.c_int32),
+        ("Seed", C.c_int64),
+    ]
+
+    def __repr__(self):
+        return ("TVdxSamplerConfig(Temperature=%r, TopK=%r, TopP=%r, MinP=%r, RepeatPenalty=%r, "
+                "RepeatWindow=%r, Seed=%r)" % (self.Temperature, self.TopK, self.TopP, self.MinP,
+                                               self.RepeatPenalty, self.RepeatWindow, self.Seed))
+
+
+class _Outputs(C.Structure):
+    _fields_ = [
+        ("tokens", C.c_void_p),
+        ("topk_idx", C.c_void_p),
+        ("topk_prob", C.c_void_p),
+        ("topk_stride", C.c_int32),
+        ("flags", C.c_void_p),
+        ("uniforms", C.c_void_p),
+    ]
+
+
+_lib = None
+
+# Every entry point declared in include/vdx_sampler.h, with its ctypes signature.
+_SIGNATURES = {
+    "vdx_sampler_default_config": (None, [C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_create": (C.c_int, [C.POINTER(C.c_void_p), C.c_int32, C.c_int32]),
+    "vdx_sampler_destroy": (None, [C.c_void_p]),
+    "vdx_sampler_set_config": (C.c_int, [C.c_void_p, C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_get_config": (C.c_int, [C.c_void_p, C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_process": (C.c_int32, [C.c_void_p, C.POINTER(C.c_float), C.c_int32]),
+    "vdx_sampler_process_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                             C.c_int64, C.c_void_p, C.POINTER(_Outputs),
+                                             C.c_void_p]),
+    "vdx_sampler_add_to_history": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32]),
+    "vdx_sampler_add_to_history_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32,
+                                                    C.c_void_p]),
+    "vdx_sampler_reset_history": (C.c_int, [C.c_void_p, C.c_int32]),
+    "vdx_sampler_set_history": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_int32), C.c_int32,
+                                          C.c_int32]),
+    "vdx_sampler_get_history": (C.c_int32, [C.c_void_p, C.c_int32, C.POINTER(C.c_int32),
+                                            C.c_int32, C.POINTER(C.c_int32)]),
+    "vdx_sampler_set_rng": (C.c_int, [C.c_void_p, C.c_int32]),
+    "vdx_sampler_last_error": (C.c_char_p, [C.c_void_p]),
+    "vdx_sampler_version": (C.c_char_p, []),
+}
+
+
+def lib_path() -> str:
+    return _build.LIB
+
+
+def load_library():
+    """Loads libvdxsampler.so (built by vindexllm_amd.build); raises if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_build.LIB):
+            raise RuntimeError(f"{_build.LIB} is not built; run __graft_entry__.build()")
+        L = C.CDLL(_build.LIB)
+        for name, (res, args) in _SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _err(s) -> str:
+    m = load_library().vdx_sampler_last_error(s)
+    return m.decode() if m else ""
+
+
+class TVdxSampler:
+    """TVdxSampler (Sampler.pas:37-91) backed by the GPU library.
+
+    ``max_rows`` is the largest batch ``process_device`` will be given; the
+    host-pointer ``Process`` samples row 0.
+    """
+
+    def __init__(self, device: int = 0, max_rows: int = 1):
+        L = load_library()
+        h = C.c_void_p()
+        rc = L.vdx_sampler_create(C.byref(h), int(device), int(max_rows))
+        if rc != VDX_OK:
+            raise VdxSamplerError(rc, _err(None))
+        self._h = h
+        self.max_rows = int(max_rows)
+        self.device = int(device)
+        self._errors = []
+
+    # -- lifetime ---------------------------------------------------------
+    def Free(self):
+        if getattr(self, "_h", None):
+            load_library().vdx_sampler_destroy(self._h)
+            self._h = None
+
+    close = Free
+
+    def __del__(self):
+        try:
+            self.Free()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.Free()
+
+    def _check(self, rc: int) -> int:
+        if rc < 0:
+            msg = _err(self._h)
+            self._errors.append(msg)
+            raise VdxSamplerError(rc, msg)
+        return rc
+
+    def GetErrors(self):
+        """Messages of failed calls (the reference keeps a TVdxErrors list)."""
+        return list(self._errors)
+
+    # -- configuration (Sampler.pas:100-155) --------------------------------
+    @staticmethod
+    def DefaultConfig() -> TVdxSamplerConfig:
+        c = TVdxSamplerConfig()
+        load_library().vdx_sampler_default_config(C.byref(c))
+        return c
+
+    def SetConfig(self, cfg: TVdxSamplerConfig):
+        self._check(load_library().vdx_sampler_set_config(self._h, C.byref(cfg)))
+
+    def GetConfig(self) -> TVdxSamplerConfig:
+        c = TVdxSamplerConfig()
+        self._check(load_library().vdx_sampler_get_config(self._h, C.byref(c)))
+        return c
+
+    def SetRng(self, kind: int):
+        self._check(load_library().vdx_sampler_set_rng(self._h, int(kind)))
+
+    # -- sampling -------------------------------------------------------------
+    def Process(self, logits, vocab_size: int | None = None) -> int:
+        """Process (Sampler.pas:265-528) on a host float32 numpy array, which is
+        penalised in place as in the reference; returns the token id."""
+        import numpy as np
+
+        assert isinstance(logits, np.ndarray) and logits.dtype == np.float32
+        assert logits.flags["C_CONTIGUOUS"]
+        V = int(logits.shape[-1] if vocab_size is None else vocab_size)
+        ptr = logits.ctypes.data_as(C.POINTER(C.c_float))
+        return self._check(load_library().vdx_sampler_process(self._h, ptr, V))
+
+    def process_device(self, logits, uniforms=None, tokens=None, topk_idx=None, topk_prob=None,
+                       flags=None, uniforms_out=None, rows: int | None = None,
+                       vocab: int | None = None, row_stride: int | None = None, stream=None):
+        """Samples ``rows`` device-resident rows of ``logits`` (a float32 GPU
+        tensor, row r at offset r*row_stride; penalised in place).
+        ``uniforms`` (float32 GPU tensor, one per row) replaces the RNG draw.
+        Returns the int32 token tensor; asynchronous on ``stream`` (default:
+        torch's current stream)."""
+        import torch
+
+        assert logits.is_cuda and logits.dtype == torch.float32
+        if logits.dim() == 1:
+            logits = logits.view(1, -1)
+        B = int(logits.shape[0] if rows is None else rows)
+        V = int(logits.shape[-1] if vocab is None else vocab)
+        stride = int(logits.stride(0) if row_stride is None else row_stride)
+        if tokens is None:
+            tokens = torch.empty(B, dtype=torch.int32, device=logits.device)
+        o = _Outputs()
+        o.tokens = tokens.data_ptr()
+        o.topk_idx = topk_idx.data_ptr() if topk_idx is not None else None
+        o.topk_prob = topk_prob.data_ptr() if topk_prob is not None else None
+        o.topk_stride = int(topk_idx.shape[-1] if topk_idx is not None else
+                            (topk_prob.shape[-1] if topk_prob is not None else 0))
+        o.flags = flags.data_ptr() if flags is not None else None
+        o.uniforms = uniforms_out.data_ptr() if uniforms_out is not None else None
+        if uniforms is not None:
+            assert uniforms.is_cuda and uniforms.dtype == torch.float32 and uniforms.numel() >= B
+        st = stream if stream is not None else torch.cuda.current_stream(logits.device)
+        self._check(load_library().vdx_sampler_process_device(
+            self._h, C.c_void_p(logits.data_ptr()), B, V, stride,
+            C.c_void_p(uniforms.data_ptr()) if uniforms is not None else None, C.byref(o),
+            C.c_void_p(st.cuda_stream)))
+        return tokens
+
+    # -- history (Sampler.pas:530-549) ----------------------------------------
+    def AddToHistory(self, token_id: int, row: int = 0):
+        self._check(load_library().vdx_sampler_add_to_history(self._h, int(row), int(token_id)))
+
+    def add_to_history_device(self, tokens, stream=None):
+        import torch
+
+        st = stream if stream is not None else torch.cuda.current_stream(tokens.device)
+        self._check(load_library().vdx_sampler_add_to_history_device(
+            self._h, C.c_void_p(tokens.data_ptr()), int(tokens.numel()), C.c_void_p(st.cuda_stream)))
+
+    def ResetHistory(self, row: int = -1):
+        self._check(load_library().vdx_sampler_reset_history(self._h, int(row)))
+
+    def set_history(self, row: int, ids, pos: int | None = None):
+        import numpy as np
+
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        n = int(a.size)
+        p = (n % max(self.GetConfig().RepeatWindow, 1)) if pos is None else int(pos)
+        self._check(load_library().vdx_sampler_set_history(
+            self._h, int(row), a.ctypes.data_as(C.POINTER(C.c_int32)) if n else None, n, p))
+
+    def get_history(self, row: int = 0):
+        import numpy as np
+
+        cap = max(self.GetConfig().RepeatWindow, 0)
+        buf = np.zeros(max(cap, 1), dtype=np.int32)
+        pos = C.c_int32()
+        n = self._check(load_library().vdx_sampler_get_history(
+            self._h, int(row), buf.ctypes.data_as(C.POINTER(C.c_int32)), cap, C.byref(pos)))
+        return buf[:n].tolist(), pos.value
+
+
+def version() -> str:
+    return load_library().vdx_sampler_version().decode()
