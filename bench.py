@@ -1,0 +1,308 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X token-sampling path (TVdxSampler on the GPU).
+
+A step is one batched sampling call over B resident rows of V fp32 logits:
+repetition penalty (in place) + top-K select + softmax / Top-P / draw, all in
+libvdxsampler.so's HIP kernels.  Prints ONE JSON line (rank 0).
+
+Default workload (the metric's B=64, top-k 64 / top-p 0.95 configuration):
+  penalised batch, B=64, V=262144, logits 3*N(0,1) + 6 at 32 hot ids per
+  row, a 256-id history per row (half from the hot ids, half uniform), RP 1.1
+  (window 256), T 0.8, top-k 64, top-p 0.95, the sampler's own per-row RNG.
+
+Inputs are resident in HBM before timing.  Logits cycle through a pool of
+buffers totalling >= 2 GiB so no step is served from the 256 MiB MALL; the
+pool is restored from a pristine copy (outside the timed region) before each
+measured phase, so the in-place penalty (applied again each time a buffer is
+reused, as the reference does on its input) stays far from overflow.  The timed loop is K
+steps bracketed by torch.cuda.synchronize(); by default the steps are issued
+from a captured hipGraph (one node per pool buffer), the way a serving loop
+issues them; --eager issues every call from Python instead.
+
+roofline: the dominant kernel (the top-K select) is timed with HIP events
+recorded by the library on the launch stream; achieved = algorithmic bytes
+per launch (logit bytes read once, B*V*4) / its mean duration.
+cpu_baseline: the oracle (oracle/vdx_oracle.c, a C restatement of
+TVdxSampler.Process, gcc -O2) on one host core over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+METRIC = "rows/sec sampled (B=64, V=262144, topk64/topp0.95); % of HBM peak"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
+POOL_BYTES = 2 << 30
+
+WORKLOADS = {
+    "penalised_b64": dict(
+        rows=64, vocab=262144, hist=256,
+        cfg=dict(Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256, Seed=3003),
+        desc="penalised batch: B=64 V=262144 fp32 3*N(0,1)+6 at 32 hot ids/row, 256-id history/row, "
+             "RP 1.1 window 256, T 0.8, top-k 64, top-p 0.95"),
+    "topk_b256": dict(
+        rows=256, vocab=262144, hist=0,
+        cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3006),
+        desc="B=256 V=262144 fp32 3*N(0,1)+8 at 16 ids/row, T 1.0, top-k 64, top-p 0.95"),
+    "full_b256": dict(
+        rows=256, vocab=262144, hist=0,
+        cfg=dict(Temperature=0.7, TopK=0, TopP=0.9, Seed=3004),
+        desc="full-vocab B=256 V=262144 Zipf logits, T 0.7, top-k 0 (TopP ignored as in the reference)"),
+    "greedy_b64": dict(
+        rows=64, vocab=262144, hist=0, cfg=dict(Temperature=0.0, Seed=3002),
+        desc="greedy argmax B=64 V=262144, 4 tied maxima/row"),
+    "single_row": dict(
+        rows=1, vocab=262144, hist=0, cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3001),
+        desc="B=1 V=262144 fp32 3*N(0,1)+8 at 16 ids, T 1.0, top-k 64, top-p 0.95"),
+}
+DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
+                   "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
+                   "single_row": "k_topk_vec"}
+
+
+def make_inputs(name, seed=1000):
+    w = WORKLOADS[name]
+    rng = np.random.default_rng(seed)
+    B, V = w["rows"], w["vocab"]
+    hist = None
+    if name == "full_b256":
+        L = np.empty((B, V), dtype=np.float32)
+        lr = np.log(np.arange(1, V + 1, dtype=np.float64))
+        for r in range(B):
+            L[r] = (-1.1 * lr[rng.permutation(V)] + 0.5 * rng.standard_normal(V)).astype(np.float32)
+        return L, hist
+    L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+    if name == "penalised_b64":
+        hist = np.zeros((B, w["hist"]), dtype=np.int32)
+        for r in range(B):
+            hot = rng.choice(V, 32, replace=False)
+            L[r, hot] += np.float32(6.0)
+            h = np.concatenate([rng.choice(hot, w["hist"] // 2), rng.integers(0, V, w["hist"] // 2)])
+            rng.shuffle(h)
+            hist[r] = h
+    elif name == "greedy_b64":
+        for r in range(B):
+            L[r, rng.choice(V, 4, replace=False)] = L[r].max() + 1.0
+    else:
+        for r in range(B):
+            L[r, rng.choice(V, 16, replace=False)] += np.float32(8.0)
+    return L, hist
+
+
+def configure(s, w):
+    c = s.DefaultConfig()
+    for k, v in w["cfg"].items():
+        setattr(c, k, v)
+    s.SetConfig(c)
+
+
+def cpu_baseline(name, L, hist, seconds):
+    """The oracle on one host core: rows processed serially, as the
+    reference's Process does; a bounded sample of ~`seconds` of CPU work."""
+    from oracle import vdx_oracle as O
+
+    w = WORKLOADS[name]
+    c = w["cfg"]
+    cfg = O.make_config(temperature=c.get("Temperature", 0.0), top_k=c.get("TopK", 0),
+                        top_p=c.get("TopP", 1.0), min_p=c.get("MinP", 0.0),
+                        repeat_penalty=c.get("RepeatPenalty", 1.0),
+                        repeat_window=c.get("RepeatWindow", 64))
+    B = L.shape[0]
+    u = (np.random.default_rng(7).integers(0, 2**24, B) / 2**24).astype(np.float32)
+    rows_done, busy, passes = 0, 0.0, 0
+    while busy < seconds:
+        X = L.copy()
+        t0 = time.perf_counter()
+        O.process_batch(X, cfg, u, hist=hist, threads=1)
+        busy += time.perf_counter() - t0
+        rows_done += B
+        passes += 1
+    return dict(value=rows_done / busy, unit="rows/s", cores=1, kind="port",
+                sample=f"{passes} passes x {B} rows of the same workload ({busy:.1f} s), "
+                       f"oracle/vdx_oracle.c gcc -O2, 1 thread")
+
+
+def run_gpu(name, steps, warmup, eager, timing_steps):
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    w = WORKLOADS[name]
+    B, V = w["rows"], w["vocab"]
+    L, hist = make_inputs(name)
+    dev = torch.device("cuda:0")
+    step_bytes = B * V * 4
+    P = max(2, math.ceil(POOL_BYTES / step_bytes))
+    pristine = torch.from_numpy(L).to(dev)
+    pool = [pristine.clone() for _ in range(P)]
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    s = TVdxSampler(0, B)
+    configure(s, w)
+    if hist is not None:
+        for r in range(B):
+            s.set_history(r, hist[r])
+    stream = torch.cuda.current_stream(dev)
+    for i in range(max(warmup, 1)):
+        s.process_device(pool[i % P], tokens=tok, stream=stream)
+    torch.cuda.synchronize()
+
+    def restore():
+        for b in pool:
+            b.copy_(pristine)
+        torch.cuda.synchronize()
+
+    graph = None
+    if not eager:
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream(dev)
+        cs.wait_stream(stream)
+        with torch.cuda.stream(cs):
+            s.process_device(pool[0], tokens=tok, stream=cs)  # workspace already sized
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cs):
+            for i in range(P):
+                s.process_device(pool[i], tokens=tok, stream=cs)
+        torch.cuda.synchronize()
+        graph = g
+        reps = max(1, steps // P)
+        steps = reps * P
+        g.replay()
+        torch.cuda.synchronize()
+
+    restore()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if graph is not None:
+        for _ in range(steps // P):
+            graph.replay()
+    else:
+        for i in range(steps):
+            s.process_device(pool[i % P], tokens=tok, stream=stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    # dominant-kernel duration from HIP events on the launch stream
+    restore()
+    s.set_timing(True)
+    for i in range(timing_steps):
+        s.process_device(pool[i % P], tokens=tok, stream=stream)
+    k_ms, k_n = s.get_timing(0)
+    torch.cuda.synchronize()
+    s.set_timing(True)
+    for i in range(timing_steps):
+        s.process_device(pool[i % P], tokens=tok, stream=stream)
+    pen_ms, pen_n = s.get_timing(1)
+    s.set_timing(False)
+    # which path the rows took (one call on restored inputs)
+    restore()
+    fl = torch.zeros(B, dtype=torch.int32, device=dev)
+    s.process_device(pool[0], tokens=tok, flags=fl, stream=stream)
+    torch.cuda.synchronize()
+    flags = fl.cpu().numpy()
+    s.Free()
+    return dict(steps=steps, elapsed=elapsed, rows=B, vocab=V, step_bytes=step_bytes, pool=P,
+                kernel_ms=k_ms / max(k_n, 1), penalty_ms=pen_ms / max(pen_n, 1),
+                launch="hipGraph" if graph is not None else "eager",
+                fast_frac=float(((flags & 0x2) != 0).mean()),
+                replay_frac=float(((flags & 0x4) != 0).mean()))
+
+
+def copy_calibration(nbytes=1 << 30, reps=5):
+    """Device-to-device copies of a known size, for scaling rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
+    import torch
+
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def read_traffic(name):
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="penalised_b64", choices=sorted(WORKLOADS))
+    ap.add_argument("--eager", action="store_true", help="issue every step from Python")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--others", action="store_true", help="also measure the other workloads")
+    ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--timing-steps", type=int, default=200)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the sampling path has no multi-GPU "
+              "collective (rows shard with zero exchange), so --gpus must be 1", file=sys.stderr)
+        sys.exit(3)
+
+    r = run_gpu(a.workload, a.steps, a.warmup, a.eager, a.timing_steps)
+    rows_s = r["rows"] * r["steps"] / r["elapsed"]
+    ms_step = 1e3 * r["elapsed"] / r["steps"]
+    achieved = r["step_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": rows_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": r["steps"],
+        "warmup": a.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": WORKLOADS[a.workload]["desc"], "rows": r["rows"], "vocab": r["vocab"],
+                   "launch": r["launch"], "pool_buffers": r["pool"],
+                   "us_per_row": 1e3 * ms_step / r["rows"],
+                   "hbm_frac_step": (r["step_bytes"] / (ms_step * 1e-3) / 1e9) / HBM_PEAK_GBS,
+                   "penalty_kernel_us": 1e3 * r["penalty_ms"],
+                   "rows_fast_path": r["fast_frac"], "rows_replay_path": r["replay_frac"]},
+        "roofline": {"bound": "hbm", "kernel": DOMINANT_KERNEL[a.workload],
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(a.workload),
+                     "kernel_us": 1e3 * r["kernel_ms"], "bytes_per_launch": r["step_bytes"]},
+    }
+    if a.others:
+        others = {}
+        for name in WORKLOADS:
+            if name == a.workload:
+                continue
+            o = run_gpu(name, max(200, a.steps // 4), 20, a.eager, 100)
+            others[name] = {"rows_per_s": o["rows"] * o["steps"] / o["elapsed"],
+                            "us_per_step": 1e6 * o["elapsed"] / o["steps"],
+                            "kernel_us": 1e3 * o["kernel_ms"],
+                            "kernel_hbm_frac": o["step_bytes"] / (o["kernel_ms"] * 1e-3) / 1e9
+                            / HBM_PEAK_GBS}
+        out["other_workloads"] = others
+    if a.copy_calibration:
+        copy_calibration()
+    if not a.no_cpu:
+        L, hist = make_inputs(a.workload)
+        out["cpu_baseline"] = cpu_baseline(a.workload, L, hist, a.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -131,6 +131,18 @@ int32_t vdx_sampler_get_history(vdx_sampler *s, int32_t row, int32_t *ids,
 /* Selects VDX_RNG_XOSHIRO (default) or VDX_RNG_PHILOX; reseeds all rows. */
 int vdx_sampler_set_rng(vdx_sampler *s, int32_t kind);
 
+/* Instrumentation; no counterpart in the reference.  When enabled, every
+ * vdx_sampler_process_device call records HIP events on its stream before the
+ * penalty kernel, between the penalty and the sampling kernel, and after the
+ * sampling kernel (events are created here, not in the sampling call). */
+int vdx_sampler_set_timing(vdx_sampler *s, int32_t enable);
+
+/* Sum (ms) and count of the recorded durations since the last query:
+ * which = 0 the sampling kernel(s), 1 the penalty kernel, 2 the whole call.
+ * Waits for the recorded events, then clears the record. */
+int vdx_sampler_get_timing(vdx_sampler *s, int32_t which, double *total_ms,
+                           int64_t *count);
+
 /* Last error message of `s` (or of the last failed create when s is NULL). */
 const char *vdx_sampler_last_error(const vdx_sampler *s);
 

@@ -375,3 +375,39 @@ def test_injected_u_leaves_rng_untouched():
         ref = O.Sampler()
         ref.set_config(O.make_config(temperature=1.0, seed=9))
         assert uo.cpu().numpy()[0] == O.lib().vdxo_u24(O.xoshiro_stream(O.seed_state(9), 1)[0])
+
+
+def test_graph_replay_matches_eager():
+    # the sampling call captured in a hipGraph and replayed several times, with
+    # eager work in between, gives the eager result every time
+    import torch
+    from vindexllm_amd import TVdxSampler
+
+    log("[case] graph replay")
+    rng = np.random.default_rng(55)
+    B, V = 16, 262144
+    L, hist = cfg3_inputs(rng, B, V, 256)
+    u = torch.from_numpy(u_stream(rng, B)).cuda()
+    pristine = torch.from_numpy(L).cuda()
+    buf = pristine.clone()
+    with TVdxSampler(0, B) as s:
+        _cfg(s, Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256, Seed=1)
+        for r in range(B):
+            s.set_history(r, hist[r])
+        tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+        eager = s.process_device(buf, uniforms=u).clone()
+        eager_logits = buf.clone()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            s.process_device(buf, uniforms=u, tokens=tok, stream=cs)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            buf.copy_(pristine)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(tok, eager), rep
+            assert torch.equal(buf, eager_logits), rep
+            _ = (pristine * 2).sum().item()  # unrelated eager work between replays

@@ -10,8 +10,9 @@
 #include <time.h>
 
 #include <string>
+#include <vector>
 
-#include "../../include/vdx_sampler.h"
+#include "vdx_sampler.h"
 #include "vdx_internal.hpp"
 
 using namespace vdx;
@@ -38,8 +39,14 @@ struct vdx_sampler {
   float *d_row = nullptr;
   int32_t row_cap = 0;
   int32_t *d_tok = nullptr;
+  // instrumentation: three events per timed call
+  bool timing = false;
+  std::vector<hipEvent_t> ev;
+  int32_t n_timed = 0;
   std::string err;
 };
+
+constexpr int32_t kTimedCalls = 4096;
 
 static std::string g_create_err;
 
@@ -151,6 +158,7 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_tickets);
   (void)hipFree(s->d_row);
   (void)hipFree(s->d_tok);
+  for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
   if (s->stream) (void)hipStreamDestroy(s->stream);
   (void)hipSetDevice(cur);
   delete s;
@@ -294,15 +302,53 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.gpart = s->d_gpart;
   p.tickets = s->d_tickets;
 
+  const bool timed = s->timing && s->n_timed < kTimedCalls;
+  hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
+  if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
   // Step 0: repetition penalty (Sampler.pas:287)
   if (c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
     HIP_TRY(s, launch_penalty(p, st));
+  if (timed) HIP_TRY(s, hipEventRecord(ev[1], st));
   if (greedy)
     HIP_TRY(s, launch_greedy(p, st));
   else if (topk)
     HIP_TRY(s, launch_topk(p, st));
   else
     HIP_TRY(s, launch_full(p, st));
+  if (timed) {
+    HIP_TRY(s, hipEventRecord(ev[2], st));
+    ++s->n_timed;
+  }
+  return VDX_OK;
+}
+
+int vdx_sampler_set_timing(vdx_sampler *s, int32_t enable) {
+  if (!s) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  if (enable && s->ev.empty()) {
+    s->ev.resize(3 * kTimedCalls);
+    for (auto &e : s->ev) HIP_TRY(s, hipEventCreate(&e));
+  }
+  s->timing = enable != 0;
+  s->n_timed = 0;
+  return VDX_OK;
+}
+
+int vdx_sampler_get_timing(vdx_sampler *s, int32_t which, double *total_ms, int64_t *count) {
+  if (!s || !total_ms || !count || which < 0 || which > 2) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  double tot = 0.0;
+  const int a = (which == 1) ? 0 : (which == 0 ? 1 : 0);
+  const int b = (which == 1) ? 1 : 2;
+  for (int32_t i = 0; i < s->n_timed; ++i) {
+    HIP_TRY(s, hipEventSynchronize(s->ev[3 * i + 2]));
+    float ms = 0.0f;
+    HIP_TRY(s, hipEventElapsedTime(&ms, s->ev[3 * i + a], s->ev[3 * i + b]));
+    tot += ms;
+  }
+  *total_ms = tot;
+  *count = s->n_timed;
+  s->n_timed = 0;
   return VDX_OK;
 }
 

@@ -14,7 +14,7 @@ constexpr int kPerThread = 64;                 // logits per thread per chunk
 constexpr int kChunk = kBlock * kPerThread;    // 16384 logits (64 KiB) per chunk
 constexpr int kWaveSpan = 64 * kPerThread;     // 4096 contiguous logits per wave
 constexpr int kKMax = 64;                      // top-K held one slot per lane
-constexpr int kCandCap = 256;                  // candidates stored per chunk
+constexpr int kCandCap = 128;                  // candidates stored per chunk
 constexpr int kMaxChunks = 256;                // V <= 4 Mi logits
 constexpr int kMergeCap = 2048;                // merge-phase LDS candidates
 constexpr int kReplayTile0 = 2048;             // first replay tile (logits)
@@ -29,26 +29,39 @@ struct RowState {
   int32_t hist_count;   // ring fill (Sampler.pas:50)
 };
 
-// Top-K stream phase: one record per (row, chunk).
+// Top-K stream phase: one record per (row, chunk), two words:
+//   w[0] = tau_key | count << 32   (every logit with key >= tau_key is stored;
+//                                   count may exceed kCandCap: overflow)
+//   w[1] = flags << 32             (flags bit 0: a NaN or +inf logit was seen)
 struct ChunkMeta {
-  uint32_t tau_key;     // every logit of the chunk with key >= tau_key is stored
-  uint32_t count;       // candidates found (may exceed kCandCap: overflow)
-  uint32_t max_key;     // chunk maximum (non-NaN) as a key
-  uint32_t flags;       // bit 0: a non-finite logit was seen
+  uint64_t w[2];
 };
 
-struct Cand {
-  float v;
-  int32_t idx;
-};
+// A stored candidate: ord_key(value) << 32 | ~index (larger = better, unique).
+typedef uint64_t Cand;
 
-// Full-softmax path: one record per (row, chunk).
+// Full-softmax path: one record per (row, chunk):
+//   w[0] = bits(m) | flags << 32  (m = chunk max of s = fl32(L * invT))
+//   w[1] = bits(d)                (sum of weights relative to m or the row max)
+//   w[2+w] = bits(dw[w])          (the same per 4096-logit wave segment)
 struct FullMeta {
-  float m;              // chunk max of s = fl32(L * invT)
-  uint32_t flags;       // bit 0: non-finite s seen
-  double d;             // sum of weights relative to m (or to the row max)
-  double dw[kWaves];    // the same per wave (4096-logit segments)
+  uint64_t w[2 + kWaves];
 };
+
+// ---- exchange between the workgroups of one launch ------------------------------
+// The records above cross workgroups (and XCDs, each with its own L2) inside
+// one kernel.  They are written and read with system-scope relaxed accesses
+// (sc0 sc1: the L2 of the writer's XCD is written through and the reader's is
+// bypassed); a writer waits for its stores to be acknowledged
+// (s_waitcnt vmcnt(0)) before taking the row's ticket, so the workgroup that
+// takes the last ticket reads complete records without an L2 writeback or
+// invalidate.
+__device__ __forceinline__ void xstore(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t xload(const uint64_t *p) {
+  return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 struct KernelRng {
   const float *uniforms;  // injected per-row u (nullable)

@@ -68,19 +68,22 @@ __device__ __forceinline__ int chunk_pos(int wv, int lane, int i) {
 }
 
 // Last-workgroup election for a row: returns true in every thread of the
-// workgroup that finished the row last.  Writes made before the call by any
-// workgroup of the row are visible to the winner after it returns.
+// workgroup that finished the row last.  Records written with xstore() before
+// the call by any workgroup of the row are complete when the winner reads them
+// with xload(): each wave waits for its stores to be acknowledged before the
+// workgroup takes its ticket.
 __device__ __forceinline__ bool last_of_row(uint32_t *tickets, int row, int nchunks, int *flag) {
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t t = atomicAdd(&tickets[row], 1u);
+    const uint32_t t = __hip_atomic_fetch_add(&tickets[row], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_SYSTEM);
     *flag = (t == (uint32_t)(nchunks - 1));
   }
   __syncthreads();
   if (!*flag) return false;
-  __threadfence();
-  if (threadIdx.x == 0) tickets[row] = 0u;  // every other chunk has arrived
+  if (threadIdx.x == 0)  // every other chunk has arrived: reset for the next launch
+    __hip_atomic_store(&tickets[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   return true;
 }
 
@@ -91,45 +94,62 @@ __device__ __forceinline__ bool last_of_row(uint32_t *tickets, int row, int nchu
 // =============================================================================
 constexpr int kPenStage = 4096;
 
+__device__ __forceinline__ float penalise(float x, int k, float pen) {
+  for (int r = 0; r < k; ++r) {
+    if (x > 0.0f)
+      x = x / pen;
+    else if (x < 0.0f)
+      x = x * pen;
+  }
+  return x;
+}
+
 __global__ __launch_bounds__(kBlock) void k_penalty(float *__restrict__ logits, int64_t stride,
                                                     int32_t V, const int32_t *__restrict__ hist,
                                                     int32_t W, const RowState *__restrict__ rs,
                                                     float pen) {
-  __shared__ int32_t sh[kPenStage];
+  __shared__ __align__(16) int32_t sh[kPenStage];
   const int row = blockIdx.x;
   const int cnt = min(rs[row].hist_count, W);
   if (cnt <= 0) return;
   const int32_t *h = hist + (int64_t)row * W;
   float *L = logits + (int64_t)row * stride;
-  const bool staged = cnt <= kPenStage;
-  if (staged) {
-    for (int j = threadIdx.x; j < cnt; j += kBlock) sh[j] = h[j];
-    __syncthreads();
-  }
-  for (int j = threadIdx.x; j < cnt; j += kBlock) {
-    const int id = staged ? sh[j] : h[j];
-    if (id < 0 || id >= V) continue;
-    int k = 0;
-    bool first = true;
-    for (int jj = 0; jj < cnt; ++jj) {
-      const int o = staged ? sh[jj] : h[jj];
-      if (o == id) {
-        if (jj < j) {
-          first = false;
-          break;
+  if (cnt > kPenStage) {
+    // long windows: the same rule with the ids read from HBM
+    for (int j = threadIdx.x; j < cnt; j += kBlock) {
+      const int id = h[j];
+      if (id < 0 || id >= V) continue;
+      int k = 0;
+      bool first = true;
+      for (int jj = 0; jj < cnt; ++jj) {
+        if (h[jj] == id) {
+          if (jj < j) {
+            first = false;
+            break;
+          }
+          ++k;
         }
-        ++k;
       }
+      if (first) L[id] = penalise(L[id], k, pen);
     }
-    if (!first) continue;
-    float x = L[id];
-    for (int r = 0; r < k; ++r) {
-      if (x > 0.0f)
-        x = x / pen;
-      else if (x < 0.0f)
-        x = x * pen;
+    return;
+  }
+  const int cnt4 = (cnt + 3) & ~3;
+  for (int j = threadIdx.x; j < cnt4; j += kBlock) sh[j] = (j < cnt) ? h[j] : -1;
+  __syncthreads();
+  const int4 *s4 = reinterpret_cast<const int4 *>(sh);
+  for (int j = threadIdx.x; j < cnt; j += kBlock) {
+    const int id = sh[j];
+    if (id < 0 || id >= V) continue;  // padding (-1) never matches an in-range id
+    int total = 0, before = 0;
+    for (int q = 0; q < cnt4 / 4; ++q) {
+      const int4 w = s4[q];  // every lane reads the same word: LDS broadcast
+      const int b = 4 * q;
+      total += (w.x == id) + (w.y == id) + (w.z == id) + (w.w == id);
+      before += (w.x == id && b < j) + (w.y == id && b + 1 < j) + (w.z == id && b + 2 < j) +
+                (w.w == id && b + 3 < j);
     }
-    L[id] = x;
+    if (before == 0) L[id] = penalise(L[id], total, pen);  // first occurrence applies all
   }
 }
 
@@ -168,12 +188,12 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
     uint64_t k = s_w[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
-    p.gpart[(int64_t)row * p.nchunks + chunk] = k;
+    xstore(&p.gpart[(int64_t)row * p.nchunks + chunk], k);
   }
   if (!last_of_row(p.tickets, row, p.nchunks, &s_last)) return;
   uint64_t k = 0;
   for (int c = tid; c < p.nchunks; c += kBlock) {
-    const uint64_t x = p.gpart[(int64_t)row * p.nchunks + c];
+    const uint64_t x = xload(&p.gpart[(int64_t)row * p.nchunks + c]);
     k = x > k ? x : k;
   }
   k = wave_max_u64(k);
@@ -220,9 +240,14 @@ struct TopkSmem {
   uint32_t wtot[kWaves];
   int32_t last;
   uint32_t ccount[kMaxChunks];
-  uint32_t n, n2;
+  uint32_t ctau[kMaxChunks];
+  uint32_t n;
+  uint32_t hist[256];
+  uint32_t rbin, rneed, rcnt;
+  uint32_t ngt;
   int32_t ntop;
-  uint64_t topkey[kKMax + 1];
+  uint64_t topsel[kKMax];
+  uint64_t topkey[kKMax];
   float uval;
   int32_t token;
   uint32_t rowflags;
@@ -240,7 +265,6 @@ struct TopkSmem {
   float q_ord[kKMax];
   int32_t i_ord[kKMax];
   float v_ord[kKMax];
-  uint64_t sk2[512];
   union {
     uint64_t sk[kMergeCap];
     struct {
@@ -250,47 +274,67 @@ struct TopkSmem {
   } buf;
 };
 
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Per-chunk candidate quota.  A chunk stores every logit >= tau_c, where tau_c
+// guarantees >= Kq stored logits.  The merge proves afterwards that the stored
+// set holds the row's top K (theta = K-th largest stored value >= every tau_c)
+// or re-reads the chunks for which that fails, so Kq may be far below K: the
+// row's top 64 holds about 64/S logits of each of its S chunks.
+__device__ __forceinline__ int chunk_quota(int K, int S) {
+  if (S <= 1 || S * kCandCap > kMergeCap) return K;
+  const int q = (3 * K + S - 1) / S + 4;
+  return min(K, max(8, q));
+}
+
 template <bool VEC>
-__device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0, int clen, int K,
+__device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0, int clen, int Kq,
                                             Cand *__restrict__ cand, ChunkMeta *__restrict__ meta,
                                             TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const bool full = (clen == kChunk);
+  constexpr int kG = kPerThread / 4;
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
 
-  // thread maximum and a non-finite detector (inf*0 and NaN*0 are NaN)
-  float m = -INFINITY, nf = 0.0f;
-  bool hasv = full;
-  if (full) {
-    m = v[0];
+  // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
+  // so a NaN or +inf anywhere in the thread's logits shows in `m`
+  float gm[kG];
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      m = fmaxf(m, v[i]);
-      nf = __builtin_fmaf(v[i], 0.0f, nf);
-    }
-  } else {
+  for (int j = 0; j < kG; ++j)
+    gm[j] = vmax(vmax(vmax(v[4 * j], v[4 * j + 1]), v[4 * j + 2]), v[4 * j + 3]);
+  float m = gm[0];
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      if (chunk_pos(wv, lane, i) < clen) {
-        hasv = true;
-        m = fmaxf(m, v[i]);
-        nf = __builtin_fmaf(v[i], 0.0f, nf);
-      }
-    }
-  }
+  for (int j = 1; j < kG; ++j) m = vmax(m, gm[j]);
+  const bool hasv = chunk_pos(wv, lane, 0) < clen;
+  const bool bad = hasv && !(m <= 3.4028235e38f);
   const uint32_t mk = hasv ? ord_key(m) : 0u;
-  const uint64_t badw = __ballot(nf != nf);
-  const uint32_t wm = wave_max_u32(mk);
-  if (lane == 0) {
-    sm.wmax[wv] = wm;
-    sm.wflag[wv] = badw != 0ull;
+  const uint64_t badw = __ballot(bad);
+  // Full chunks with a quota of at most 16: every wave finds its R-th largest
+  // thread maximum (R knock-out rounds of a wave max); tau = the smallest of
+  // the four, so >= 4R >= Kq thread maxima (distinct logits) reach tau.
+  const bool fastthr = (clen == kChunk) && Kq <= 4 * kWaves;
+  if (fastthr) {
+    const int R = (Kq + kWaves - 1) / kWaves;
+    uint32_t key = mk, rth = 0u;
+    for (int r = 0; r < R; ++r) {
+      const uint32_t mx = wave_max_u32(key);
+      rth = mx;
+      const uint64_t who = __ballot(key == mx);
+      if (lane == __ffsll((unsigned long long)who) - 1) key = 0u;
+    }
+    if (lane == 0) sm.wmax[wv] = rth;
+  } else if (wv == 0) {
+    sm.thr[lane] = mk;
   }
-  if (wv == 0) sm.thr[lane] = mk;
+  if (lane == 0) sm.wflag[wv] = badw != 0ull;
   __syncthreads();
 
-  uint32_t tau = 0u;  // 0: store every logit of a short chunk
-  if (clen > kCandCap) {
+  // tau: 0 stores every logit of a short chunk
+  uint32_t tau = 0u;
+  if (fastthr) {
+    tau = min(min(sm.wmax[0], sm.wmax[1]), min(sm.wmax[2], sm.wmax[3]));
+  } else if (clen > kCandCap) {
+    // the largest of 64 sampled thread maxima (wave 0's) that >= Kq reach
     uint32_t mycnt = 0u;
 #pragma unroll 8
     for (int j = 0; j < 64; ++j) {
@@ -302,25 +346,31 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
     __syncthreads();
     const uint32_t tot = sm.cnt[0][lane] + sm.cnt[1][lane] + sm.cnt[2][lane] + sm.cnt[3][lane];
     const uint32_t tk = sm.thr[lane];
-    tau = wave_max_u32((tot >= (uint32_t)K && tk != 0u) ? tk : 0u);
+    tau = wave_max_u32((tot >= (uint32_t)Kq && tk != 0u) ? tk : 0u);
   }
   const float tf = key_float(tau);
 
-  // candidate extraction: 4-bit masks per float4 group, then ordered writes
-  uint32_t mlo = 0u, mhi = 0u;
+  // candidates: test float4 group maxima first, logits only in passing groups
+  uint32_t gmask = 0u;
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
-    bool pass;
-    if (full)
-      pass = v[i] >= tf;
-    else
-      pass = (chunk_pos(wv, lane, i) < clen) && (tau == 0u || v[i] >= tf);
-    if (i < 32)
-      mlo |= pass ? (1u << i) : 0u;
-    else
-      mhi |= pass ? (1u << (i - 32)) : 0u;
+  for (int j = 0; j < kG; ++j) {
+    const bool gv = chunk_pos(wv, lane, 4 * j) < clen;
+    const bool gp = gv && (tau == 0u || gm[j] >= tf);
+    gmask |= gp ? (1u << j) : 0u;
   }
-  const uint32_t c = (uint32_t)(__popc(mlo) + __popc(mhi));
+  uint32_t c = 0u;
+  if (gmask) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      if ((gmask >> j) & 1u) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool pv = chunk_pos(wv, lane, 4 * j + e) < clen;
+          c += (pv && (tau == 0u || v[4 * j + e] >= tf)) ? 1u : 0u;
+        }
+      }
+    }
+  }
   const uint32_t incl = wave_incl_scan_u32(c);
   if (lane == 63) sm.wtot[wv] = incl;
   __syncthreads();
@@ -333,14 +383,15 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
   uint32_t pos = base + incl - c;
   if (c) {
 #pragma unroll
-    for (int j = 0; j < kPerThread / 4; ++j) {
-      const uint32_t g = ((j < 8) ? (mlo >> (4 * j)) : (mhi >> (4 * (j - 8)))) & 0xFu;
-      if (g) {
+    for (int j = 0; j < kG; ++j) {
+      if ((gmask >> j) & 1u) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if ((g >> e) & 1u) {
+          const int cp = chunk_pos(wv, lane, 4 * j + e);
+          if (cp < clen && (tau == 0u || v[4 * j + e] >= tf)) {
             if (pos < (uint32_t)kCandCap)
-              cand[pos] = Cand{v[4 * j + e], c0 + chunk_pos(wv, lane, 4 * j + e)};
+              xstore(&cand[pos], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
+                                     (uint32_t)(~(uint32_t)(c0 + cp)));
             ++pos;
           }
         }
@@ -348,122 +399,268 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
     }
   }
   if (tid == 0) {
-    ChunkMeta cm;
-    cm.tau_key = tau;
-    cm.count = total;
-    cm.max_key = max(max(sm.wmax[0], sm.wmax[1]), max(sm.wmax[2], sm.wmax[3]));
-    cm.flags = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
-    *meta = cm;
+    const uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
+    xstore(&meta->w[0], (uint64_t)tau | ((uint64_t)total << 32));
+    xstore(&meta->w[1], (uint64_t)fl << 32);
   }
 }
 
-// Merge phase.  Returns false when the row must be replayed (non-finite
-// logits, a chunk overflowed its candidate store, or LDS capacity exceeded).
-__device__ bool topk_merge(int S, int K, const ChunkMeta *__restrict__ cm,
-                           const Cand *__restrict__ cand_row, TopkSmem &sm) {
+// Radix select (8 bits per pass, most significant first) of the K-th largest
+// value key among the n keys in sm.buf.sk.  Returns that value key; sm.rcnt
+// logits share it and sm.rneed of them are in the top K.
+// Bytes above the highest byte in which kmin and kmax (bounds of the keys)
+// differ are common to every key and are not scanned.
+__device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, TopkSmem &sm, uint32_t kmin,
+                                              uint32_t kmax) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  uint32_t mt = 0u, fl = 0u, ovf = 0u;
-  for (int c = tid; c < S; c += kBlock) {
-    const ChunkMeta x = cm[c];
-    mt = max(mt, x.tau_key);
-    fl |= x.flags;
-    ovf |= (x.count > (uint32_t)kCandCap) ? 1u : 0u;
-    sm.ccount[c] = min(x.count, (uint32_t)kCandCap);
+  const uint32_t d = kmin ^ kmax;
+  if (d == 0u) {  // every key shares one value
+    if (tid == 0) {
+      sm.rcnt = n;
+      sm.rneed = (uint32_t)K;
+    }
+    __syncthreads();
+    return kmax;
   }
-  mt = wave_max_u32(mt);
-  fl = wave_or_u32(fl);
-  ovf = wave_or_u32(ovf);
-  if (lane == 0) {
-    sm.cnt[0][wv] = mt;
-    sm.cnt[1][wv] = fl;
-    sm.cnt[2][wv] = ovf;
+  const int top = (31 - __clz((int)d)) & ~7;  // first byte that varies
+  uint32_t pmask = (top == 24) ? 0u : (0xFFFFFFFFu << (top + 8));
+  uint32_t prefix = kmax & pmask, need = (uint32_t)K;
+  for (int shift = top; shift >= 0; shift -= 8) {
+    sm.hist[tid] = 0u;
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += kBlock) {
+      const uint32_t k = (uint32_t)(sm.buf.sk[i] >> 32);
+      if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // lane l holds bins 255-4l .. 252-4l (descending values)
+      const int b0 = 255 - 4 * lane;
+      const uint32_t h0 = sm.hist[b0], h1 = sm.hist[b0 - 1], h2 = sm.hist[b0 - 2],
+                     h3 = sm.hist[b0 - 3];
+      const uint32_t sum = h0 + h1 + h2 + h3;
+      const uint32_t incl = wave_incl_scan_u32(sum);
+      const uint32_t excl = incl - sum;
+      if (excl < need && incl >= need) {
+        uint32_t above = excl, bin, cnt;
+        if (above + h0 >= need) {
+          bin = b0;
+          cnt = h0;
+        } else if (above + h0 + h1 >= need) {
+          above += h0;
+          bin = b0 - 1;
+          cnt = h1;
+        } else if (above + h0 + h1 + h2 >= need) {
+          above += h0 + h1;
+          bin = b0 - 2;
+          cnt = h2;
+        } else {
+          above += h0 + h1 + h2;
+          bin = b0 - 3;
+          cnt = h3;
+        }
+        sm.rbin = bin;
+        sm.rneed = need - above;
+        sm.rcnt = cnt;
+      }
+    }
+    __syncthreads();
+    prefix |= sm.rbin << shift;
+    pmask |= 255u << shift;
+    need = sm.rneed;
   }
+  return prefix;
+}
+
+// Merge phase (last workgroup of the row).  One round trip loads the chunk
+// records and every candidate slot into LDS; a radix select finds theta, the
+// K-th largest stored value.  The stored set holds the row's top K (and every
+// logit tied with theta) when theta >= tau_c for every chunk c, since a logit
+// that was not stored is < tau_c.  Chunks where that fails (or whose store
+// overflowed) are re-read from HBM against theta, a lower bound of the row's
+// K-th value, and theta is recomputed.  Returns false when the row must be
+// replayed: non-finite logits, LDS capacity exceeded, or the K-th value is
+// tied with a logit outside the set.
+template <bool VEC>
+__device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, int S, int K,
+                           const ChunkMeta *__restrict__ cm, const Cand *__restrict__ cand_row,
+                           TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int kSpec = 8;
+  const int nslots = S * kCandCap;
   if (tid == 0) sm.n = 0u;
+  uint32_t fl = 0u;
+  for (int c = tid; c < S; c += kBlock) {
+    const uint64_t w0 = xload(&cm[c].w[0]), w1 = xload(&cm[c].w[1]);
+    const uint32_t count = (uint32_t)(w0 >> 32);
+    fl |= (uint32_t)(w1 >> 32);
+    sm.ccount[c] = min(count, (uint32_t)kCandCap);
+    // a chunk is "open" (must be re-read) when its store overflowed
+    sm.ctau[c] = (count > (uint32_t)kCandCap) ? 0xFFFFFFFFu : (uint32_t)w0;
+  }
+  uint64_t kk[kSpec];
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int r = 0; r < kSpec; ++r) {
+    const int i = tid + r * kBlock;
+    kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
+  }
+  fl = wave_or_u32(fl);
+  if (lane == 0) sm.cnt[1][wv] = fl;
   __syncthreads();
-  mt = max(max(sm.cnt[0][0], sm.cnt[0][1]), max(sm.cnt[0][2], sm.cnt[0][3]));
   fl = sm.cnt[1][0] | sm.cnt[1][1] | sm.cnt[1][2] | sm.cnt[1][3];
-  ovf = sm.cnt[2][0] | sm.cnt[2][1] | sm.cnt[2][2] | sm.cnt[2][3];
-  __syncthreads();
-  if (fl || ovf) return false;
-
-  // gather candidates >= max tau: kBlock/S threads per chunk
-  const int tpc = kBlock / S;
-  const int c = tid / tpc, sub = tid - c * tpc;
-  if (c < S) {
-    const uint32_t nc = sm.ccount[c];
-    for (uint32_t e = (uint32_t)sub; e < nc; e += (uint32_t)tpc) {
-      const Cand x = cand_row[(int64_t)c * kCandCap + e];
-      const uint32_t k = ord_key(x.v);
-      if (k >= mt) {
-        const uint32_t p = atomicAdd(&sm.n, 1u);
-        if (p < (uint32_t)kMergeCap) sm.buf.sk[p] = ((uint64_t)k << 32) | (uint32_t)(~(uint32_t)x.idx);
+  if (fl) return false;
+  for (int base = 0; base < nslots; base += kSpec * kBlock) {
+    if (base > 0) {
+#pragma unroll
+      for (int r = 0; r < kSpec; ++r) {
+        const int i = base + tid + r * kBlock;
+        kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kSpec; ++r) {
+      const int i = base + tid + r * kBlock;
+      if (i < nslots) {
+        const int c = i / kCandCap, e = i - c * kCandCap;
+        if ((uint32_t)e < sm.ccount[c]) {
+          const uint32_t q = atomicAdd(&sm.n, 1u);
+          if (q < (uint32_t)kMergeCap) sm.buf.sk[q] = kk[r];
+          kmin = min(kmin, (uint32_t)(kk[r] >> 32));
+          kmax = max(kmax, (uint32_t)(kk[r] >> 32));
+        }
       }
     }
   }
+  kmin = wave_min_u32(kmin);
+  kmax = wave_max_u32(kmax);
+  if (lane == 0) {
+    sm.cnt[2][wv] = kmin;
+    sm.cnt[3][wv] = kmax;
+  }
   __syncthreads();
-  const uint32_t n = sm.n;
+  kmin = min(min(sm.cnt[2][0], sm.cnt[2][1]), min(sm.cnt[2][2], sm.cnt[2][3]));
+  kmax = max(max(sm.cnt[3][0], sm.cnt[3][1]), max(sm.cnt[3][2], sm.cnt[3][3]));
+  uint32_t n = sm.n;
   if (n > (uint32_t)kMergeCap) return false;
+  uint32_t theta = (n >= (uint32_t)K) ? radix_kth(n, K, sm, kmin, kmax) : 0u;
 
-  const uint64_t *src = sm.buf.sk;
-  uint32_t n2 = n;
-  if (n > 128u) {
-    // second sampled threshold over the gathered keys
-    if (wv == 0) sm.thr[lane] = (uint32_t)(sm.buf.sk[lane] >> 32);
-    if (tid == 0) sm.n2 = 0u;
-    __syncthreads();
-    const int nr = (int)((n + kBlock - 1) / kBlock);
-    uint32_t mycnt = 0u;
-    for (int r = 0; r < nr; ++r) {
+  // chunks whose unstored logits could still reach theta
+  for (int round = 0; round < 2; ++round) {
+    int open = 0;
+    for (int c = tid; c < S; c += kBlock) open |= (sm.ctau[c] > theta) ? 1 : 0;
+    open = __syncthreads_or(open);
+    if (!open) break;
+    if (round == 1) return false;  // cannot happen: re-read chunks are closed
+    // keep stored keys >= theta of closed chunks, then re-read open chunks
+    uint64_t keep[kMergeCap / kBlock];
+#pragma unroll
+    for (int r = 0; r < kMergeCap / kBlock; ++r) {
       const uint32_t i = (uint32_t)(tid + r * kBlock);
-      const uint32_t key = (i < n) ? (uint32_t)(sm.buf.sk[i] >> 32) : 0u;
-      for (int j = 0; j < 64; ++j) {
-        const uint32_t cj = (uint32_t)__popcll(__ballot(key >= sm.thr[j]));
-        mycnt += (lane == j) ? cj : 0u;
-      }
-    }
-    sm.cnt[wv][lane] = mycnt;
-    __syncthreads();
-    const uint32_t tot = sm.cnt[0][lane] + sm.cnt[1][lane] + sm.cnt[2][lane] + sm.cnt[3][lane];
-    const uint32_t t2 = wave_max_u32(tot >= (uint32_t)K ? sm.thr[lane] : 0u);
-    for (int r = 0; r < nr; ++r) {
-      const uint32_t i = (uint32_t)(tid + r * kBlock);
+      keep[r] = 0ull;
       if (i < n) {
         const uint64_t k = sm.buf.sk[i];
-        if ((uint32_t)(k >> 32) >= t2) {
-          const uint32_t q = atomicAdd(&sm.n2, 1u);
-          if (q < 512u) sm.sk2[q] = k;
+        const int c = (int)((~(uint32_t)k) / (uint32_t)kChunk);
+        if ((uint32_t)(k >> 32) >= theta && sm.ctau[c] <= theta) keep[r] = k;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) sm.n = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kMergeCap / kBlock; ++r) {
+      if (keep[r]) {
+        const uint32_t q = atomicAdd(&sm.n, 1u);
+        sm.buf.sk[q] = keep[r];  // at most the previous n entries
+      }
+    }
+    for (int c = 0; c < S; ++c) {
+      if (sm.ctau[c] <= theta) continue;  // uniform
+      const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+      if (VEC && clen == kChunk) {
+#pragma nounroll
+        for (int jb = 0; jb < kPerThread / 4; jb += 4) {  // four float4 loads in flight
+          const int l0 = wv * kWaveSpan + jb * 256 + lane * 4;
+          const f32x4 f0 = *reinterpret_cast<const f32x4 *>(L + c0 + l0);
+          const f32x4 f1 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 256);
+          const f32x4 f2 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 512);
+          const f32x4 f3 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 768);
+          const f32x4 fs[4] = {f0, f1, f2, f3};
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = fs[jj][e];
+              if (ord_key(x) >= theta) {
+                const uint32_t q = atomicAdd(&sm.n, 1u);
+                if (q < (uint32_t)kMergeCap)
+                  sm.buf.sk[q] = ((uint64_t)ord_key(x) << 32) |
+                                 (uint32_t)(~(uint32_t)(c0 + l0 + jj * 256 + e));
+              }
+            }
+          }
+        }
+      } else {
+#pragma nounroll
+        for (int i = 0; i < kPerThread; ++i) {
+          const int local = chunk_pos(wv, lane, i);
+          if (local < clen) {
+            const float x = L[c0 + local];
+            if (ord_key(x) >= theta) {
+              const uint32_t q = atomicAdd(&sm.n, 1u);
+              if (q < (uint32_t)kMergeCap)
+                sm.buf.sk[q] = ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)(c0 + local));
+            }
+          }
         }
       }
     }
     __syncthreads();
-    n2 = sm.n2;
-    src = sm.sk2;
-    if (n2 > 512u) return false;
+    for (int c = tid; c < S; c += kBlock)
+      if (sm.ctau[c] > theta) sm.ctau[c] = theta;  // now closed
+    n = sm.n;
+    if (n > (uint32_t)kMergeCap) return false;
+    theta = radix_kth(n, K, sm, 0u, 0xFFFFFFFFu);
   }
-  // rank sort by (value desc, index asc); keys are unique
-  for (int r = 0; r < 2; ++r) {
-    const uint32_t i = (uint32_t)(tid + r * kBlock);
-    if (i < n2) {
-      const uint64_t key = src[i];
-      uint32_t rank = 0u;
-      for (uint32_t j = 0; j < n2; ++j) rank += (src[j] > key) ? 1u : 0u;
-      if (rank <= (uint32_t)K) sm.topkey[rank] = key;
+  if (n < (uint32_t)K) return false;
+  // `need` of the rcnt logits valued theta are in the top K
+  if (sm.rcnt > sm.rneed) return false;  // the K-th value is tied outside the set
+  if (tid == 0) sm.ngt = 0u;
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += kBlock) {
+    const uint64_t k = sm.buf.sk[i];
+    if ((uint32_t)(k >> 32) >= theta) {
+      const uint32_t q = atomicAdd(&sm.ngt, 1u);
+      if (q < (uint32_t)kKMax) sm.topsel[q] = k;
     }
   }
-  if (tid == 0) sm.ntop = (int32_t)min(n2, (uint32_t)(K + 1));
+  __syncthreads();
+  if (tid < K) {  // exactly K selected: rank by (value desc, index asc)
+    const uint64_t key = sm.topsel[tid];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += (sm.topsel[j] > key) ? 1 : 0;
+    sm.topkey[rank] = key;
+  }
+  if (tid == 0) sm.ntop = K;
   __syncthreads();
   return true;
 }
 
-// Fast finish over the sorted top-K (wave 0).  Sets sm.replay when the
-// exactness conditions do not hold.
-__device__ void topk_fast(const CallParams &p, int row, TopkSmem &sm) {
+// Fast finish over the sorted top-K.  With Top-P < 1 the reference draws in
+// the stable descending order of q (Sampler.pas:412-459); sorting by value
+// gives that order up to permutations inside groups of equal q, which only
+// matter if the Top-P cut splits such a group or the draw lands in one -- those
+// rows (and Top-P >= 1, NaN/inf, non-positive invT) are replayed.  When every
+// non-zero q is within 2^22 of the largest, every fp64 partial sum of q is
+// exact, so wave-parallel scans give the reference's sums bit for bit;
+// otherwise the sums are accumulated sequentially in the draw order as the
+// reference does, with the initial sum S (slot order in the reference) taken
+// in value order (equal up to a few ulp).
+__device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int K = p.top_k;
   if (tid < 64) {
-    bool elig = (p.top_p < 1.0f) && (p.inv_t > 0.0f) && (p.inv_t <= 3.4028235e38f) && (sm.ntop >= K);
-    if (sm.ntop > K && (uint32_t)(sm.topkey[K] >> 32) == (uint32_t)(sm.topkey[K - 1] >> 32))
-      elig = false;  // the K-th value is tied outside the set
+    bool elig = (p.top_p < 1.0f) && (p.inv_t > 0.0f) && (p.inv_t <= 3.4028235e38f) && (sm.ntop == K);
     const bool act = lane < K;
     const uint64_t sk = act ? sm.topkey[lane] : 0ull;
     const float val = key_float((uint32_t)(sk >> 32));
@@ -471,48 +668,127 @@ __device__ void topk_fast(const CallParams &p, int row, TopkSmem &sm) {
     const float M = key_float((uint32_t)(sm.topkey[0] >> 32));
     float q = 0.0f;
     if (act) q = (float)exp(((double)val - (double)M) * (double)p.inv_t);
+    const bool bad = act && !(q <= 3.4028235e38f);
+    elig = elig && (__ballot(bad) == 0ull);
     const float qmax = __shfl(q, 0);
     const float qfloor = ldexpf(qmax, -22);
-    bool bad = act && !(q == 0.0f || (q <= 3.4028235e38f && q >= qfloor));
-    const float qn = __shfl_down(q, 1);
-    bad = bad || ((lane + 1 < K) && qn != 0.0f && qn == q);
-    if (p.min_p > 0.0f) {
-      const float thr = qmax * p.min_p;
-      if (q < thr) q = 0.0f;
-    }
-    const double s1 = wave_sum_f64((double)q);
-    const double target = (double)p.top_p * s1;
-    const double incl = wave_incl_scan_f64((double)q);
-    const double excl = incl - (double)q;
-    const float qk = (excl < target && q > 0.0f) ? q : 0.0f;
-    const double s2 = wave_sum_f64((double)qk);
-    elig = elig && (__ballot(bad) == 0ull) && (s2 > 0.0);
-    if (elig) {
-      const double t = (double)sm.uval * s2;
+    const bool exact = __ballot(act && !(q == 0.0f || q >= qfloor)) == 0ull;
+    if (elig && exact) {
+      if (p.min_p > 0.0f) {  // Min-P (:393-410): Qmax = q[0]
+        const float thr = qmax * p.min_p;
+        if (q < thr) q = 0.0f;
+      }
+      const double S = wave_sum_f64((double)q);
+      const double target = (double)p.top_p * S;
+      const double incl = wave_incl_scan_f64((double)q);
+      const bool kept = act && ((incl - (double)q) < target) && q > 0.0f;  // Top-P (:431-444)
+      const float qk = kept ? q : 0.0f;
+      const double S2 = wave_sum_f64((double)qk);
+      const double t = (double)sm.uval * S2;  // draw (:447-459)
       const double c2 = wave_incl_scan_f64((double)qk);
       const uint64_t hit = __ballot(act && c2 > t);
-      const int first = hit ? (__ffsll((unsigned long long)hit) - 1) : (K - 1);
-      const int32_t tok = __shfl(idx, first);
-      if (lane == 0) {
-        sm.token = tok;
-        sm.rowflags = kRowTopkFast | (hit ? 0u : kRowFallback);
-        sm.replay = 0;
+      const int pos = hit ? (__ffsll((unsigned long long)hit) - 1) : -1;
+      const uint64_t dropm = __ballot(act && !kept);
+      const int cut = dropm ? (__ffsll((unsigned long long)dropm) - 1) : K;
+      const float qprev = __shfl_up(q, 1), qnext = __shfl_down(q, 1);
+      const bool split = (lane == cut) && cut > 0 && q > 0.0f && q == qprev;
+      const bool tie = (lane == pos) && ((lane > 0 && qprev == q) || (lane + 1 < K && qnext == q));
+      const bool amb = (pos < 0) || (__ballot(split || tie) != 0ull);
+      const int32_t tok = __shfl(idx, pos < 0 ? 0 : pos);  // every lane takes part
+      if (!amb) {
+        if (lane == 0) {
+          sm.token = tok;
+          sm.rowflags = kRowTopkFast;
+          sm.replay = 0;
+        }
+        if (act) {
+          const int64_t o = (int64_t)row * p.out.topk_stride + lane;
+          if (p.out.topk_idx) p.out.topk_idx[o] = idx;
+          if (p.out.topk_prob) p.out.topk_prob[o] = (float)((double)qk / S2);
+        }
+      } else if (lane == 0) {
+        sm.replay = 1;
       }
+      if (lane == 0) sm.qnan = 0;  // parallel finish done
+    } else {
       if (act) {
-        const int64_t o = (int64_t)row * p.out.topk_stride + lane;
-        if (p.out.topk_idx) p.out.topk_idx[o] = idx;
-        if (p.out.topk_prob) p.out.topk_prob[o] = (float)((double)qk / s2);
+        sm.q[lane] = q;
+        sm.i_ord[lane] = idx;
       }
-    } else if (lane == 0) {
-      sm.replay = 1;
+      if (lane == 0) {
+        sm.replay = elig ? 0 : 1;
+        sm.qnan = 1;  // sequential finish pending
+      }
     }
   }
   __syncthreads();
+  if (!sm.qnan) return;
+  if (tid == 0 && !sm.replay) {
+    // Min-P (:393-410): Qmax is q[0]; zero q < fl32(Qmax * MinP)
+    double S = 0.0;
+    for (int k = 0; k < K; ++k) S = S + (double)sm.q[k];
+    if (p.min_p > 0.0f) {
+      const float thr = sm.q[0] * p.min_p;
+      S = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (sm.q[k] < thr)
+          sm.q[k] = 0.0f;
+        else
+          S = S + (double)sm.q[k];
+      }
+    }
+    // Top-P (:431-444)
+    const double target = (double)p.top_p * S;
+    double C = 0.0, S2 = 0.0;
+    int cut = K;
+    for (int k = 0; k < K; ++k) {
+      const float qk = sm.q[k];
+      if (C < target && qk > 0.0f) {
+        C = C + (double)qk;
+        S2 = S2 + (double)qk;
+        sm.q_ord[k] = qk;
+      } else {
+        if (cut == K) cut = k;
+        sm.q_ord[k] = 0.0f;
+      }
+    }
+    bool amb = (cut > 0 && cut < K) && sm.q[cut] > 0.0f && sm.q[cut] == sm.q[cut - 1];
+    // draw (:447-459)
+    const double t = (double)sm.uval * S2;
+    C = 0.0;
+    int pos = -1;
+    for (int k = 0; k < K; ++k) {
+      C = C + (double)sm.q_ord[k];
+      if (C > t) {
+        pos = k;
+        break;
+      }
+    }
+    if (pos < 0) {
+      amb = true;  // S' = 0: the fallback picks by slot order
+    } else {
+      const float qp = sm.q[pos];
+      amb = amb || (pos > 0 && sm.q[pos - 1] == qp) || (pos + 1 < K && sm.q[pos + 1] == qp);
+    }
+    if (amb) {
+      sm.replay = 1;
+    } else {
+      sm.token = sm.i_ord[pos];
+      sm.rowflags = kRowTopkFast;
+      sm.S = S2;
+    }
+  }
+  __syncthreads();
+  if (!sm.replay && tid < K) {
+    const int64_t o = (int64_t)row * p.out.topk_stride + tid;
+    if (p.out.topk_idx) p.out.topk_idx[o] = sm.i_ord[tid];
+    if (p.out.topk_prob) p.out.topk_prob[o] = (float)((double)sm.q_ord[tid] / sm.S);
+  }
 }
 
 // Exact replay of the reference min-buffer (Sampler.pas:341-383) and the
 // slot-order finish (:385-459).  Whole workgroup.
-__device__ void topk_replay(const CallParams &p, int row, TopkSmem &sm) {
+__device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int K = p.top_k, V = p.vocab;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -764,14 +1040,14 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
-  topk_stream<VEC>(L, c0, clen, K, cr + (int64_t)chunk * kCandCap, cm + chunk, sm);
+  topk_stream<VEC>(L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap, cm + chunk, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
   if (threadIdx.x == 0) {
     sm.uval = draw_uniform(p.rng, row);
     sm.replay = 1;
   }
   __syncthreads();
-  if (topk_merge(S, K, cm, cr, sm)) topk_fast(p, row, sm);
+  if (topk_merge<VEC>(L, p.vocab, S, K, cm, cr, sm)) topk_fast(p, row, sm);
   if (sm.replay) topk_replay(p, row, sm);
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
@@ -843,8 +1119,9 @@ __global__ __launch_bounds__(kBlock) void k_full_max(CallParams p) {
   __syncthreads();
   if (tid == 0) {
     FullMeta *fm = p.fmeta + (int64_t)row * p.nchunks + chunk;
-    fm->m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-    fm->flags = s_f[0] | s_f[1] | s_f[2] | s_f[3];
+    const float mc = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    const uint32_t fc = s_f[0] | s_f[1] | s_f[2] | s_f[3];
+    xstore(&fm->w[0], (uint64_t)__float_as_uint(mc) | ((uint64_t)fc << 32));
   }
 }
 
@@ -879,7 +1156,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   if (EXACT) {
     // row maximum from the k_full_max records of this row
     float mm = -INFINITY;
-    for (int c = tid; c < S; c += kBlock) mm = fmaxf(mm, fm[c].m);
+    for (int c = tid; c < S; c += kBlock) mm = fmaxf(mm, __uint_as_float((uint32_t)xload(&fm[c].w[0])));
     mm = wave_max_f32(mm);
     if (lane == 0) sm.wm[wv] = mm;
     __syncthreads();
@@ -916,13 +1193,13 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
     double d = 0.0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      me->dw[w] = sm.wd[w];
+      xstore(&me->w[2 + w], (uint64_t)__double_as_longlong(sm.wd[w]));
       d = d + sm.wd[w];
     }
-    me->d = d;
+    xstore(&me->w[1], (uint64_t)__double_as_longlong(d));
     if (!EXACT) {
-      me->m = base;
-      me->flags = sm.wf[0] | sm.wf[1] | sm.wf[2] | sm.wf[3];
+      const uint32_t fc = sm.wf[0] | sm.wf[1] | sm.wf[2] | sm.wf[3];
+      xstore(&me->w[0], (uint64_t)__float_as_uint(base) | ((uint64_t)fc << 32));
     }
   }
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
@@ -933,9 +1210,10 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   uint32_t fl = 0u;
   double dc = 0.0;
   if (tid < S) {
-    mc = fm[tid].m;
-    fl = fm[tid].flags;
-    dc = fm[tid].d;
+    const uint64_t w0 = xload(&fm[tid].w[0]);
+    mc = __uint_as_float((uint32_t)w0);
+    fl = (uint32_t)(w0 >> 32);
+    dc = __longlong_as_double((long long)xload(&fm[tid].w[1]));
   }
   const float wmx = wave_max_f32(mc);
   const uint32_t wfl = wave_or_u32(fl);
@@ -984,12 +1262,15 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
     if (cs < 0) cs = S - 1;
   }
   // segment of the target chunk (4096-logit wave spans), sequentially
-  const FullMeta tc = fm[cs];
-  const double scale = EXACT ? 1.0 : exp((double)tc.m - (double)M);
+  const float tcm = __uint_as_float((uint32_t)xload(&fm[cs].w[0]));
+  double tdw[kWaves];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) tdw[w] = __longlong_as_double((long long)xload(&fm[cs].w[2 + w]));
+  const double scale = EXACT ? 1.0 : exp((double)tcm - (double)M);
   double before = cs ? sm.cincl[cs - 1] : 0.0;
   int ws_ = -1;
   for (int w = 0; w < kWaves; ++w) {
-    const double ww = tc.dw[w] * scale;
+    const double ww = tdw[w] * scale;
     if (before + ww > t) {
       ws_ = w;
       break;
@@ -999,10 +1280,10 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   if (ws_ < 0) {
     ws_ = kWaves - 1;
     before = cs ? sm.cincl[cs - 1] : 0.0;
-    for (int w = 0; w < kWaves - 1; ++w) before = before + tc.dw[w] * scale;
-    while (ws_ > 0 && tc.dw[ws_] == 0.0) {
+    for (int w = 0; w < kWaves - 1; ++w) before = before + tdw[w] * scale;
+    while (ws_ > 0 && tdw[ws_] == 0.0) {
       --ws_;
-      before = before - tc.dw[ws_] * scale;
+      before = before - tdw[ws_] * scale;
     }
   }
   // rescan that segment: thread tid owns 16 consecutive logits
@@ -1020,7 +1301,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
         const float q = (float)exp((double)s - (double)M);
         w = (q < p.min_p) ? 0.0f : q;
       } else {
-        w = expf(s - tc.m);
+        w = expf(s - tcm);
       }
     }
     w16[i] = w;

@@ -93,6 +93,9 @@ _SIGNATURES = {
     "vdx_sampler_get_history": (C.c_int32, [C.c_void_p, C.c_int32, C.POINTER(C.c_int32),
                                             C.c_int32, C.POINTER(C.c_int32)]),
     "vdx_sampler_set_rng": (C.c_int, [C.c_void_p, C.c_int32]),
+    "vdx_sampler_set_timing": (C.c_int, [C.c_void_p, C.c_int32]),
+    "vdx_sampler_get_timing": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_double),
+                                         C.POINTER(C.c_int64)]),
     "vdx_sampler_last_error": (C.c_char_p, [C.c_void_p]),
     "vdx_sampler_version": (C.c_char_p, []),
 }
@@ -235,6 +238,19 @@ class TVdxSampler:
             C.c_void_p(uniforms.data_ptr()) if uniforms is not None else None, C.byref(o),
             C.c_void_p(st.cuda_stream)))
         return tokens
+
+    # -- instrumentation ------------------------------------------------------
+    def set_timing(self, enable: bool):
+        self._check(load_library().vdx_sampler_set_timing(self._h, 1 if enable else 0))
+
+    def get_timing(self, which: int = 0):
+        """(total_ms, count) of the event-timed sampling kernels (which=0),
+        penalty kernels (1) or whole calls (2) since the last query."""
+        t = C.c_double()
+        n = C.c_int64()
+        self._check(load_library().vdx_sampler_get_timing(self._h, int(which), C.byref(t),
+                                                           C.byref(n)))
+        return t.value, n.value
 
     # -- history (Sampler.pas:530-549) ----------------------------------------
     def AddToHistory(self, token_id: int, row: int = 0):
