@@ -64,7 +64,7 @@ WORKLOADS = {
         rows=1, vocab=262144, hist=0, cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3001),
         desc="B=1 V=262144 fp32 3*N(0,1)+8 at 16 ids, T 1.0, top-k 64, top-p 0.95"),
 }
-DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
+DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec_pen", "topk_b256": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec"}
 
@@ -275,7 +275,8 @@ def main():
                    "launch": r["launch"], "pool_buffers": r["pool"],
                    "us_per_row": 1e3 * ms_step / r["rows"],
                    "hbm_frac_step": (r["step_bytes"] / (ms_step * 1e-3) / 1e9) / HBM_PEAK_GBS,
-                   "penalty_kernel_us": 1e3 * r["penalty_ms"],
+                   "penalty": ("fused into the top-K kernel" if WORKLOADS[a.workload]["cfg"].get("RepeatPenalty", 1.0) != 1.0
+                               and WORKLOADS[a.workload]["cfg"].get("TopK", 0) > 0 else "none"),
                    "rows_fast_path": r["fast_frac"], "rows_replay_path": r["replay_frac"]},
         "roofline": {"bound": "hbm", "kernel": DOMINANT_KERNEL[a.workload],
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

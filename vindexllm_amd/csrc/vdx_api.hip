@@ -302,12 +302,14 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.gpart = s->d_gpart;
   p.tickets = s->d_tickets;
 
+  // Step 0: repetition penalty (Sampler.pas:287); the top-K kernel applies
+  // it itself for windows of up to kPenMax ids
+  const bool pen = c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0;
+  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
-  // Step 0: repetition penalty (Sampler.pas:287)
-  if (c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
-    HIP_TRY(s, launch_penalty(p, st));
+  if (pen && !p.fuse_penalty) HIP_TRY(s, launch_penalty(p, st));
   if (timed) HIP_TRY(s, hipEventRecord(ev[1], st));
   if (greedy)
     HIP_TRY(s, launch_greedy(p, st));

@@ -20,6 +20,7 @@ constexpr int kMergeCap = 2048;                // merge-phase LDS candidates
 constexpr int kReplayTile0 = 2048;             // first replay tile (logits)
 constexpr int kReplayTile = 4096;              // later replay tiles (logits)
 constexpr int kReplayCap = 2048;               // replay candidates per batch
+constexpr int kPenMax = 1024;                  // history ids handled inside the top-K kernel
 
 // ---- per-row state kept in HBM -------------------------------------------------
 struct RowState {
@@ -61,6 +62,16 @@ __device__ __forceinline__ void xstore(uint64_t *p, uint64_t v) {
 }
 __device__ __forceinline__ uint64_t xload(const uint64_t *p) {
   return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// Logits written in place by the fused penalty are stored with xstoref and
+// re-read (replay, chunk re-read) with xloadf.
+__device__ __forceinline__ void xstoref(float *p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float xloadf(const float *p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(p)),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
 }
 
 struct KernelRng {

@@ -23,6 +23,7 @@ struct CallParams {
   float penalty;
   const int32_t *hist;  // [max_rows * hist_len]
   int32_t hist_len;
+  int32_t fuse_penalty; // the top-K kernel applies the penalty itself
   KernelRng rng;
   KernelOut out;
   // workspace

@@ -18,6 +18,18 @@ namespace vdx {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Four logits read past the caches (see xloadf); p is 16-byte aligned.
+__device__ __forceinline__ f32x4 xload4(const float *p) {
+  const uint64_t a = xload(reinterpret_cast<const uint64_t *>(p));
+  const uint64_t b = xload(reinterpret_cast<const uint64_t *>(p) + 1);
+  f32x4 r;
+  r[0] = __uint_as_float((uint32_t)a);
+  r[1] = __uint_as_float((uint32_t)(a >> 32));
+  r[2] = __uint_as_float((uint32_t)b);
+  r[3] = __uint_as_float((uint32_t)(b >> 32));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v |= (uint32_t)__shfl_xor((int)v, o);
@@ -265,12 +277,18 @@ struct TopkSmem {
   float q_ord[kKMax];
   int32_t i_ord[kKMax];
   float v_ord[kKMax];
+  uint32_t pbits[kChunk / 32];  // fused penalty: positions of the chunk it changed
+  uint32_t pm, pen_n;
   union {
     uint64_t sk[kMergeCap];
     struct {
       float v[kReplayCap];
       int32_t i[kReplayCap];
     } rc;
+    struct {  // fused penalty (stream phase only)
+      uint64_t key[kPenMax];
+      int32_t id[kPenMax];
+    } pen;
   } buf;
 };
 
@@ -287,14 +305,89 @@ __device__ __forceinline__ int chunk_quota(int K, int S) {
   return min(K, max(8, q));
 }
 
-template <bool VEC>
-__device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0, int clen, int Kq,
-                                            Cand *__restrict__ cand, ChunkMeta *__restrict__ meta,
-                                            TopkSmem &sm) {
+// Repetition penalty fused into the stream phase (Sampler.pas:285-303).  The
+// row's history (count and window) is loaded before the chunk's logits, so it
+// arrives first; the ids that fall in this chunk are gathered in LDS and
+// counted; one representative per distinct id applies the reference's sign
+// test and divide / multiply once per occurrence to the value in HBM, stores
+// the result in place, marks the position and lists (id, new value).  The
+// stream phase then skips marked positions and stores every listed value as a
+// candidate, so the register copies are never patched.
+constexpr int kPenPerThread = kPenMax / kBlock;
+
+struct PenaltyPrefetch {
+  int cnt;
+  int32_t id[kPenPerThread];
+};
+
+__device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
+  const int W = p.hist_len;
+  const int32_t *h = p.hist + (int64_t)row * W;
+  pf.cnt = p.rng.rows[row].hist_count;
+#pragma unroll
+  for (int r = 0; r < kPenPerThread; ++r) {
+    const int t = threadIdx.x + r * kBlock;
+    pf.id[r] = (t < W) ? h[t] : -1;
+  }
+}
+
+// Leaves sm.pen_n listed (key of the new value, index) pairs in sm.pen_key.
+__device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int c0, int clen,
+                                              const PenaltyPrefetch &pf, TopkSmem &sm) {
+  const int tid = threadIdx.x;
+  float *L = p.logits + (int64_t)row * p.stride;
+  const int cnt = min(pf.cnt, p.hist_len);
+  for (int w = tid; w < kChunk / 32; w += kBlock) sm.pbits[w] = 0u;
+  if (tid == 0) {
+    sm.pm = 0u;
+    sm.pen_n = 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kPenPerThread; ++r) {
+    const int t = tid + r * kBlock;
+    const int id = pf.id[r];
+    if (t < cnt && id >= c0 && id < c0 + clen) {
+      const uint32_t q = atomicAdd(&sm.pm, 1u);
+      sm.buf.pen.id[q] = id;  // q < cnt <= window <= kPenMax
+    }
+  }
+  __syncthreads();
+  const int m = (int)sm.pm;
+  for (int e = tid; e < m; e += kBlock) {
+    const int id = sm.buf.pen.id[e];
+    int k = 0;
+    bool rep = true;
+    for (int f = 0; f < m; ++f) {
+      if (sm.buf.pen.id[f] == id) {
+        rep = rep && (f >= e);
+        ++k;
+      }
+    }
+    if (rep) {
+      const float x = penalise(L[id], k, p.penalty);
+      xstoref(&L[id], x);
+      atomicOr(&sm.pbits[(id - c0) >> 5], 1u << ((id - c0) & 31));
+      const uint32_t q = atomicAdd(&sm.pen_n, 1u);
+      sm.buf.pen.key[q] = ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)id);
+    }
+  }
+  __syncthreads();
+}
+
+template <bool VEC, bool PEN>
+__device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
+                                            int c0, int clen, int Kq, Cand *__restrict__ cand,
+                                            ChunkMeta *__restrict__ meta, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
+  PenaltyPrefetch pf;
+  const bool pen = PEN && p.fuse_penalty != 0;
+  if (pen) penalty_prefetch(p, row, pf);
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  if (pen) fused_penalty(p, row, c0, clen, pf, sm);
+  const uint32_t npen = pen ? sm.pen_n : 0u;
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
@@ -358,14 +451,18 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
     const bool gp = gv && (tau == 0u || gm[j] >= tf);
     gmask |= gp ? (1u << j) : 0u;
   }
+  // positions changed by the fused penalty are stored from its list instead
+  uint64_t pmask = 0ull;  // 4 bits per float4 group
   uint32_t c = 0u;
   if (gmask) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
       if ((gmask >> j) & 1u) {
+        const int l0 = chunk_pos(wv, lane, 4 * j);
+        if (PEN && npen) pmask |= (uint64_t)((sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu) << (4 * j);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool pv = chunk_pos(wv, lane, 4 * j + e) < clen;
+          const bool pv = (l0 + e < clen) && !((pmask >> (4 * j + e)) & 1ull);
           c += (pv && (tau == 0u || v[4 * j + e] >= tf)) ? 1u : 0u;
         }
       }
@@ -381,6 +478,11 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
     total += sm.wtot[w];
   }
   uint32_t pos = base + incl - c;
+  if (PEN) {
+    for (uint32_t i = tid; i < npen; i += kBlock)  // penalised logits, unconditionally
+      if (total + i < (uint32_t)kCandCap) xstore(&cand[total + i], sm.buf.pen.key[i]);
+    total += npen;
+  }
   if (c) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
@@ -388,7 +490,7 @@ __device__ __forceinline__ void topk_stream(const float *__restrict__ L, int c0,
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int cp = chunk_pos(wv, lane, 4 * j + e);
-          if (cp < clen && (tau == 0u || v[4 * j + e] >= tf)) {
+          if (cp < clen && !((pmask >> (4 * j + e)) & 1ull) && (tau == 0u || v[4 * j + e] >= tf)) {
             if (pos < (uint32_t)kCandCap)
               xstore(&cand[pos], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
                                      (uint32_t)(~(uint32_t)(c0 + cp)));
@@ -581,10 +683,10 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
 #pragma nounroll
         for (int jb = 0; jb < kPerThread / 4; jb += 4) {  // four float4 loads in flight
           const int l0 = wv * kWaveSpan + jb * 256 + lane * 4;
-          const f32x4 f0 = *reinterpret_cast<const f32x4 *>(L + c0 + l0);
-          const f32x4 f1 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 256);
-          const f32x4 f2 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 512);
-          const f32x4 f3 = *reinterpret_cast<const f32x4 *>(L + c0 + l0 + 768);
+          const f32x4 f0 = xload4(L + c0 + l0);
+          const f32x4 f1 = xload4(L + c0 + l0 + 256);
+          const f32x4 f2 = xload4(L + c0 + l0 + 512);
+          const f32x4 f3 = xload4(L + c0 + l0 + 768);
           const f32x4 fs[4] = {f0, f1, f2, f3};
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
@@ -605,7 +707,7 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
         for (int i = 0; i < kPerThread; ++i) {
           const int local = chunk_pos(wv, lane, i);
           if (local < clen) {
-            const float x = L[c0 + local];
+            const float x = xloadf(&L[c0 + local]);
             if (ord_key(x) >= theta) {
               const uint32_t q = atomicAdd(&sm.n, 1u);
               if (q < (uint32_t)kMergeCap)
@@ -800,10 +902,11 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
   uint32_t skey = 0xFFFFFFFFu, mkey = 0xFFFFFFFFu;
   int mi = 0;
   float tmax = -INFINITY;
-  const bool frozen = (L[0] != L[0]);  // NaN in slot 0: nothing ever enters
+  const float l0v = xloadf(&L[0]);
+  const bool frozen = (l0v != l0v);  // NaN in slot 0: nothing ever enters
   if (wv == 0) {
     if (lane < K) {
-      sv = L[lane];
+      sv = xloadf(&L[lane]);
       si = lane;
       skey = slot_key(sv);
       tmax = fmaxf(tmax, sv);
@@ -827,7 +930,7 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
 #pragma unroll
       for (int j = 0; j < kJ; ++j) {
         const int e = j * kBlock + tid;
-        v[j] = (e < tl) ? L[t0 + e] : __builtin_nanf("");
+        v[j] = (e < tl) ? xloadf(&L[t0 + e]) : __builtin_nanf("");
       }
 #pragma unroll
       for (int j = 0; j < kJ; ++j) {
@@ -1029,7 +1132,7 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
   }
 }
 
-template <bool VEC>
+template <bool VEC, bool PEN>
 __device__ __forceinline__ void topk_body(const CallParams &p) {
   __shared__ TopkSmem sm;
   int row, chunk;
@@ -1040,7 +1143,8 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
-  topk_stream<VEC>(L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap, cm + chunk, sm);
+  topk_stream<VEC, PEN>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
+                        cm + chunk, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
   if (threadIdx.x == 0) {
     sm.uval = draw_uniform(p.rng, row);
@@ -1056,8 +1160,9 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
 }
 
 // 16-byte aligned rows: four workgroups per CU (<= 128 VGPRs, no spills).
-__global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true>(p); }
-__global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_body<false>(p); }
+__global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true, false>(p); }
+__global__ __launch_bounds__(kBlock, 4) void k_topk_vec_pen(CallParams p) { topk_body<true, true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_body<false, true>(p); }
 
 // =============================================================================
 // Full-softmax path (Sampler.pas:461-527): s = fl32(L*invT), M = max s,
@@ -1403,7 +1508,9 @@ hipError_t launch_greedy(const CallParams &p, hipStream_t st) {
 }
 
 hipError_t launch_topk(const CallParams &p, hipStream_t st) {
-  if (p.vec)
+  if (p.vec && p.fuse_penalty)
+    hipLaunchKernelGGL(k_topk_vec_pen, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  else if (p.vec)
     hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
   else
     hipLaunchKernelGGL(k_topk_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
