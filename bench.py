@@ -19,9 +19,12 @@ steps bracketed by torch.cuda.synchronize(); by default the steps are issued
 from a captured hipGraph (one node per pool buffer), the way a serving loop
 issues them; --eager issues every call from Python instead.
 
-roofline: the dominant kernel (the top-K select) is timed with HIP events
-recorded by the library on the launch stream; achieved = algorithmic bytes
-per launch (logit bytes read once, B*V*4) / its mean duration.
+roofline: each step is one kernel launch; HIP events recorded on the launch
+stream around the timed region give its mean duration; achieved = algorithmic
+bytes per launch (logit bytes read once, B*V*4) / that duration.  traffic =
+HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by
+the same counter's reading for a 1 GiB device copy (bench.py --traffic-from
+turns the two counter CSVs into profiles/traffic_<workload>.json).
 cpu_baseline: the oracle (oracle/vdx_oracle.c, a C restatement of
 TVdxSampler.Process, gcc -O2) on one host core over a bounded sample.
 """
@@ -131,7 +134,7 @@ def cpu_baseline(name, L, hist, seconds):
                        f"oracle/vdx_oracle.c gcc -O2, 1 thread")
 
 
-def run_gpu(name, steps, warmup, eager, timing_steps):
+def run_gpu(name, steps, warmup, eager):
     import torch
 
     from vindexllm_amd import TVdxSampler
@@ -179,29 +182,26 @@ def run_gpu(name, steps, warmup, eager, timing_steps):
         torch.cuda.synchronize()
 
     restore()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     if graph is not None:
         for _ in range(steps // P):
             graph.replay()
     else:
         for i in range(steps):
             s.process_device(pool[i % P], tokens=tok, stream=stream)
+    ev1.record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    # Every step of these workloads is ONE kernel launch (penalty fused into the
+    # top-K kernel, no separate max pass), so the events bracketing the timed
+    # region on the launch stream give the kernel's mean duration (plus the
+    # inter-node gap of the graph, which makes the figure conservative).
+    kernel_ms = ev0.elapsed_time(ev1) / steps
 
-    # dominant-kernel duration from HIP events on the launch stream
-    restore()
-    s.set_timing(True)
-    for i in range(timing_steps):
-        s.process_device(pool[i % P], tokens=tok, stream=stream)
-    k_ms, k_n = s.get_timing(0)
-    torch.cuda.synchronize()
-    s.set_timing(True)
-    for i in range(timing_steps):
-        s.process_device(pool[i % P], tokens=tok, stream=stream)
-    pen_ms, pen_n = s.get_timing(1)
-    s.set_timing(False)
     # which path the rows took (one call on restored inputs)
     restore()
     fl = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -210,7 +210,7 @@ def run_gpu(name, steps, warmup, eager, timing_steps):
     flags = fl.cpu().numpy()
     s.Free()
     return dict(steps=steps, elapsed=elapsed, rows=B, vocab=V, step_bytes=step_bytes, pool=P,
-                kernel_ms=k_ms / max(k_n, 1), penalty_ms=pen_ms / max(pen_n, 1),
+                kernel_ms=kernel_ms,
                 launch="hipGraph" if graph is not None else "eager",
                 fast_frac=float(((flags & 0x2) != 0).mean()),
                 replay_frac=float(((flags & 0x4) != 0).mean()))
@@ -226,6 +226,61 @@ def copy_calibration(nbytes=1 << 30, reps=5):
     for _ in range(reps):
         b.copy_(a)
     torch.cuda.synchronize()
+
+
+PMC_COMMAND = ("timeout -s KILL 60 rocprofv3 --pmc {counter} -f csv -d gpurun_out/pmc_{tag}_{workload} -o {tag} -- "
+               "python -u bench.py --workload {workload} --eager --steps 20 --warmup 3 --no-cpu "
+               "--copy-calibration")
+
+
+def _kernel_base(name):
+    name = name.strip()
+    if name.startswith("void "):
+        name = name[5:]
+    name = name.split("(")[0].strip()
+    return name[5:] if name.startswith("vdx::") else name
+
+
+def _counter_rows(path, counter):
+    import csv
+
+    with open(path, newline="") as f:
+        return [(_kernel_base(r["Kernel_Name"]), float(r["Counter_Value"]))
+                for r in csv.DictReader(f) if r["Counter_Name"] == counter]
+
+
+def traffic_from(workload, fetch_csv, write_csv, calib_bytes=1 << 30):
+    """Scale FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the dominant kernel
+    by what the same counters read for a device copy of calib_bytes, and write
+    profiles/traffic_<workload>.json."""
+    kernel = DOMINANT_KERNEL[workload]
+    out = {"workload": workload, "kernel": kernel, "calibration_copy_bytes": calib_bytes,
+           "algorithmic_bytes_per_launch": WORKLOADS[workload]["rows"] * WORKLOADS[workload]["vocab"] * 4}
+    total = 0.0
+    for counter, path, tag in (("FETCH_SIZE", fetch_csv, "fetch"), ("WRITE_SIZE", write_csv, "write")):
+        rows = _counter_rows(path, counter)
+        kern = sorted(v for k, v in rows if k == kernel)
+        copies = [v for k, v in rows if "copyBuffer" in k]
+        if not kern or not copies:
+            raise SystemExit(f"{path}: no {counter} rows for {kernel} or for the calibration copy")
+        calib = max(copies)  # the calib_bytes copies are the largest copy dispatches
+        factor = calib_bytes / (calib * 1024.0)
+        med = kern[len(kern) // 2]
+        out[f"{tag}_kib_per_dispatch_raw"] = med
+        out[f"{tag}_dispatches"] = len(kern)
+        out[f"{tag}_calibration_kib_raw"] = calib
+        out[f"{tag}_scale"] = factor
+        out[f"{tag}_bytes_per_launch"] = med * 1024.0 * factor
+        out[f"{tag}_command"] = PMC_COMMAND.format(counter=counter, tag=tag, workload=workload)
+        total += med * 1024.0 * factor
+    out["traffic_bytes_per_launch"] = total
+    out["traffic_over_algorithmic"] = total / out["algorithmic_bytes_per_launch"]
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    dst = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    with open(dst, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out))
 
 
 def read_traffic(name):
@@ -247,14 +302,18 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--others", action="store_true", help="also measure the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--timing-steps", type=int, default=200)
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU: turn two rocprofv3 --pmc counter CSVs into profiles/traffic_<workload>.json")
     a = ap.parse_args()
+    if a.traffic_from:
+        traffic_from(a.workload, *a.traffic_from)
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the sampling path has no multi-GPU "
               "collective (rows shard with zero exchange), so --gpus must be 1", file=sys.stderr)
         sys.exit(3)
 
-    r = run_gpu(a.workload, a.steps, a.warmup, a.eager, a.timing_steps)
+    r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
     ms_step = 1e3 * r["elapsed"] / r["steps"]
     achieved = r["step_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
@@ -288,7 +347,7 @@ def main():
         for name in WORKLOADS:
             if name == a.workload:
                 continue
-            o = run_gpu(name, max(200, a.steps // 4), 20, a.eager, 100)
+            o = run_gpu(name, max(200, a.steps // 4), 20, a.eager)
             others[name] = {"rows_per_s": o["rows"] * o["steps"] / o["elapsed"],
                             "us_per_step": 1e6 * o["elapsed"] / o["steps"],
                             "kernel_us": 1e3 * o["kernel_ms"],
