@@ -11,6 +11,15 @@
  * semantics follow the reference compiled for Win64 with Delphi's default
  * excess precision: Single sub-expressions feeding Exp() are evaluated in
  * double; every value stored into a Single is rounded to binary32.
+ *
+ * Pinning (tests/test_oracle_pins.py): the PRNG by published known answers
+ * and an independent numpy restatement, Philox by numpy's bit generator,
+ * penalty / greedy / top-K slots by brute force, the softmax tail and the
+ * full path by an independent numpy restatement and closed forms, the
+ * stateful object by the reference's own testbed invariants.  Parity
+ * unpinned: the last-ulp bits of Delphi's System.Exp (this file uses the C
+ * library's exp), the excess-precision choice for (v - M) * invT, and the
+ * Seed = 0 timer stream (taken as an argument here).
  */
 #ifndef VDX_ORACLE_H
 #define VDX_ORACLE_H

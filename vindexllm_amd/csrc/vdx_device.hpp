@@ -113,59 +113,97 @@ __device__ __forceinline__ uint32_t slot_key(float x) {
 }
 
 // ---- wave64 primitives --------------------------------------------------------------
+// Cross-lane steps use DPP (row_shr within 16-lane rows, then row_bcast:15 /
+// row_bcast:31 across rows), which run on the VALU without a trip through the
+// LDS crossbar.  Every primitive here must be called with all 64 lanes
+// active: the results are read from lane 63.
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint64_t dpp64(uint64_t old, uint64_t v) {
+  const uint32_t lo = dpp32<CTRL, ROWMASK>((uint32_t)old, (uint32_t)v);
+  const uint32_t hi = dpp32<CTRL, ROWMASK>((uint32_t)(old >> 32), (uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t readlane32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  return ((uint64_t)readlane32((uint32_t)(v >> 32), l) << 32) | readlane32((uint32_t)v, l);
+}
+
+// Inclusive prefix (lane 0 first) of an associative operation with identity
+// `id`: Hillis-Steele over shifts 1, 2, 4, 8 inside each row, then the row
+// totals of rows 0 / 2 into rows 1 / 3 and of rows 0-1 into rows 2-3.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_scan(T v, T id, Op op) {
+  if constexpr (sizeof(T) == 4) {
+    v = op(v, dpp32<0x111, 0xF>(id, v));
+    v = op(v, dpp32<0x112, 0xF>(id, v));
+    v = op(v, dpp32<0x114, 0xF>(id, v));
+    v = op(v, dpp32<0x118, 0xF>(id, v));
+    v = op(v, dpp32<0x142, 0xA>(id, v));
+    v = op(v, dpp32<0x143, 0xC>(id, v));
+  } else {
+    v = op(v, dpp64<0x111, 0xF>(id, v));
+    v = op(v, dpp64<0x112, 0xF>(id, v));
+    v = op(v, dpp64<0x114, 0xF>(id, v));
+    v = op(v, dpp64<0x118, 0xF>(id, v));
+    v = op(v, dpp64<0x142, 0xA>(id, v));
+    v = op(v, dpp64<0x143, 0xC>(id, v));
+  }
   return v;
+}
+struct OpMaxU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+struct OpMinU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct OpAddU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
+struct OpOrU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a | b; } };
+struct OpMaxU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
+struct OpAddF64 {
+  __device__ uint64_t operator()(uint64_t a, uint64_t b) const {
+    return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) + __longlong_as_double((long long)b));
+  }
+};
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return readlane32(wave_scan<uint32_t>(v, 0u, OpMaxU32()), 63);
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o));
-  return v;
+  return readlane32(wave_scan<uint32_t>(v, 0xFFFFFFFFu, OpMinU32()), 63);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  return readlane32(wave_scan<uint32_t>(v, 0u, OpOrU32()), 63);
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor((unsigned long long)v, o);
-    v = w > v ? w : v;
-  }
-  return v;
+  return readlane64(wave_scan<uint64_t>(v, 0ull, OpMaxU64()), 63);
 }
+// Maximum ignoring NaN (fmaxf): the ordered keys of non-NaN values, NaN as
+// the lowest key; an all-NaN wave yields NaN.
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  const uint32_t b = __float_as_uint(v);
+  uint32_t k = (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  k = wave_max_u32(k);
+  if (k == 0u) return __uint_as_float(0x7FC00000u);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
-  return v;
+  return readlane32(wave_scan<uint32_t>(v, 0u, OpAddU32()), 63);
 }
-// Inclusive scans (Hillis-Steele over the 64 lanes).
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint32_t w = (uint32_t)__shfl_up((int)v, o);
-    if (l >= o) v += w;
-  }
-  return v;
+  return wave_scan<uint32_t>(v, 0u, OpAddU32());
 }
+// Double sums: exact whenever every partial sum is representable (the
+// callers rely on this only where all addends share a 2^-52-relative grid),
+// otherwise rounded in the scan's association order.
 __device__ __forceinline__ double wave_incl_scan_f64(double v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    double w = __shfl_up(v, o);
-    if (l >= o) v += w;
-  }
-  return v;
+  return __longlong_as_double((long long)wave_scan<uint64_t>((uint64_t)__double_as_longlong(v), 0ull, OpAddF64()));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  return __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(wave_incl_scan_f64(v)), 63));
 }
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();

@@ -30,12 +30,6 @@ __device__ __forceinline__ f32x4 xload4(const float *p) {
   return r;
 }
 
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= (uint32_t)__shfl_xor((int)v, o);
-  return v;
-}
-
 // Block-wide exclusive scan of one double per thread (kBlock threads).
 __device__ __forceinline__ double block_excl_scan_f64(double x, double *wtot, double &total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -288,6 +282,7 @@ struct TopkSmem {
     struct {  // fused penalty (stream phase only)
       uint64_t key[kPenMax];
       int32_t id[kPenMax];
+      float x[kPenMax];  // the logit at id before the penalty
     } pen;
   } buf;
 };
@@ -306,18 +301,20 @@ __device__ __forceinline__ int chunk_quota(int K, int S) {
 }
 
 // Repetition penalty fused into the stream phase (Sampler.pas:285-303).  The
-// row's history (count and window) is loaded before the chunk's logits, so it
-// arrives first; the ids that fall in this chunk are gathered in LDS and
-// counted; one representative per distinct id applies the reference's sign
-// test and divide / multiply once per occurrence to the value in HBM, stores
-// the result in place, marks the position and lists (id, new value).  The
-// stream phase then skips marked positions and stores every listed value as a
-// candidate, so the register copies are never patched.
+// row's history (count and window) is loaded before the chunk's logits; once
+// it arrives, the logits at the history ids that fall in this chunk are
+// gathered (in flight together with the chunk).  The ids and values are listed
+// in LDS; one representative per distinct id applies the reference's sign test
+// and divide / multiply once per occurrence, stores the result in place, marks
+// the position and lists (key of the new value, index).  The stream phase then
+// skips marked positions and stores every listed value as a candidate, so the
+// register copies of the chunk are never patched.
 constexpr int kPenPerThread = kPenMax / kBlock;
 
 struct PenaltyPrefetch {
   int cnt;
   int32_t id[kPenPerThread];
+  float x[kPenPerThread];
 };
 
 __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
@@ -328,6 +325,19 @@ __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, P
   for (int r = 0; r < kPenPerThread; ++r) {
     const int t = threadIdx.x + r * kBlock;
     pf.id[r] = (t < W) ? h[t] : -1;
+  }
+}
+
+// Issued right after the chunk loads: the logits at this chunk's history ids.
+__device__ __forceinline__ void penalty_gather(const CallParams &p, int row, int c0, int clen,
+                                               PenaltyPrefetch &pf) {
+  const float *L = p.logits + (int64_t)row * p.stride;  // written in place below: not restrict
+  const int cnt = min(pf.cnt, p.hist_len);
+#pragma unroll
+  for (int r = 0; r < kPenPerThread; ++r) {
+    const int t = threadIdx.x + r * kBlock;
+    const int id = pf.id[r];
+    pf.x[r] = (t < cnt && id >= c0 && id < c0 + clen) ? L[id] : 0.0f;
   }
 }
 
@@ -350,6 +360,7 @@ __device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int 
     if (t < cnt && id >= c0 && id < c0 + clen) {
       const uint32_t q = atomicAdd(&sm.pm, 1u);
       sm.buf.pen.id[q] = id;  // q < cnt <= window <= kPenMax
+      sm.buf.pen.x[q] = pf.x[r];
     }
   }
   __syncthreads();
@@ -365,7 +376,7 @@ __device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int 
       }
     }
     if (rep) {
-      const float x = penalise(L[id], k, p.penalty);
+      const float x = penalise(sm.buf.pen.x[e], k, p.penalty);
       xstoref(&L[id], x);
       atomicOr(&sm.pbits[(id - c0) >> 5], 1u << ((id - c0) & 31));
       const uint32_t q = atomicAdd(&sm.pen_n, 1u);
@@ -386,6 +397,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   if (pen) penalty_prefetch(p, row, pf);
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  if (pen) penalty_gather(p, row, c0, clen, pf);
   if (pen) fused_penalty(p, row, c0, clen, pf, sm);
   const uint32_t npen = pen ? sm.pen_n : 0u;
 
@@ -443,58 +455,60 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   }
   const float tf = key_float(tau);
 
-  // candidates: test float4 group maxima first, logits only in passing groups
-  uint32_t gmask = 0u;
+  // Candidates: one wave-wide ballot per float4 group tests the group maxima;
+  // only groups in which some lane passes test their four logits (wave-uniform
+  // branches, so a wave spends ~1 VALU op on each group without candidates).
+  // Positions changed by the fused penalty are skipped here and stored from
+  // its list below.
+  const bool all = (tau == 0u);
+  uint32_t hitj = 0u, wcnt = 0u;  // wave-uniform
 #pragma unroll
   for (int j = 0; j < kG; ++j) {
-    const bool gv = chunk_pos(wv, lane, 4 * j) < clen;
-    const bool gp = gv && (tau == 0u || gm[j] >= tf);
-    gmask |= gp ? (1u << j) : 0u;
-  }
-  // positions changed by the fused penalty are stored from its list instead
-  uint64_t pmask = 0ull;  // 4 bits per float4 group
-  uint32_t c = 0u;
-  if (gmask) {
+    const int l0 = chunk_pos(wv, lane, 4 * j);
+    const bool gp = (l0 < clen) && (all || gm[j] >= tf);
+    if (__ballot(gp) != 0ull) {
+      hitj |= 1u << j;
+      uint32_t pb = 0u;
+      if (PEN && npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
 #pragma unroll
-    for (int j = 0; j < kG; ++j) {
-      if ((gmask >> j) & 1u) {
-        const int l0 = chunk_pos(wv, lane, 4 * j);
-        if (PEN && npen) pmask |= (uint64_t)((sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu) << (4 * j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool pv = (l0 + e < clen) && !((pmask >> (4 * j + e)) & 1ull);
-          c += (pv && (tau == 0u || v[4 * j + e] >= tf)) ? 1u : 0u;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
+        wcnt += (uint32_t)__popcll(__ballot(hit));
       }
     }
   }
-  const uint32_t incl = wave_incl_scan_u32(c);
-  if (lane == 63) sm.wtot[wv] = incl;
+  if (lane == 0) sm.wtot[wv] = wcnt;
   __syncthreads();
-  uint32_t base = 0u, total = 0u;
+  uint32_t pos = 0u, total = 0u;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    if (w < wv) base += sm.wtot[w];
+    if (w < wv) pos += sm.wtot[w];
     total += sm.wtot[w];
   }
-  uint32_t pos = base + incl - c;
   if (PEN) {
     for (uint32_t i = tid; i < npen; i += kBlock)  // penalised logits, unconditionally
       if (total + i < (uint32_t)kCandCap) xstore(&cand[total + i], sm.buf.pen.key[i]);
     total += npen;
   }
-  if (c) {
+  if (hitj) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
-      if ((gmask >> j) & 1u) {
+      if ((hitj >> j) & 1u) {
+        const int l0 = chunk_pos(wv, lane, 4 * j);
+        const bool gp = (l0 < clen) && (all || gm[j] >= tf);
+        uint32_t pb = 0u;
+        if (PEN && npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int cp = chunk_pos(wv, lane, 4 * j + e);
-          if (cp < clen && !((pmask >> (4 * j + e)) & 1ull) && (tau == 0u || v[4 * j + e] >= tf)) {
-            if (pos < (uint32_t)kCandCap)
-              xstore(&cand[pos], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
-                                     (uint32_t)(~(uint32_t)(c0 + cp)));
-            ++pos;
+          const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
+          const uint64_t hb = __ballot(hit);
+          if (hb) {
+            const uint32_t q = pos + __builtin_amdgcn_mbcnt_hi((uint32_t)(hb >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)hb, 0u));
+            if (hit && q < (uint32_t)kCandCap)
+              xstore(&cand[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
+                                   (uint32_t)(~(uint32_t)(c0 + l0 + e)));
+            pos += (uint32_t)__popcll(hb);
           }
         }
       }
@@ -772,7 +786,7 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
     if (act) q = (float)exp(((double)val - (double)M) * (double)p.inv_t);
     const bool bad = act && !(q <= 3.4028235e38f);
     elig = elig && (__ballot(bad) == 0ull);
-    const float qmax = __shfl(q, 0);
+    const float qmax = __uint_as_float(readlane32(__float_as_uint(q), 0));
     const float qfloor = ldexpf(qmax, -22);
     const bool exact = __ballot(act && !(q == 0.0f || q >= qfloor)) == 0ull;
     if (elig && exact) {
@@ -796,7 +810,7 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
       const bool split = (lane == cut) && cut > 0 && q > 0.0f && q == qprev;
       const bool tie = (lane == pos) && ((lane > 0 && qprev == q) || (lane + 1 < K && qnext == q));
       const bool amb = (pos < 0) || (__ballot(split || tie) != 0ull);
-      const int32_t tok = __shfl(idx, pos < 0 ? 0 : pos);  // every lane takes part
+      const int32_t tok = (int32_t)readlane32((uint32_t)idx, pos < 0 ? 0 : pos);
       if (!amb) {
         if (lane == 0) {
           sm.token = tok;
@@ -976,9 +990,9 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
             uint64_t pend = __ballot(has && ck > mkey);
             while (pend) {
               const int src = __ffsll((unsigned long long)pend) - 1;
-              const uint32_t ek = (uint32_t)__shfl((int)ck, src);
-              const float ev = __shfl(cv, src);
-              const int32_t ei = __shfl(ci, src);
+              const uint32_t ek = readlane32(ck, src);
+              const float ev = __uint_as_float(readlane32(__float_as_uint(cv), src));
+              const int32_t ei = (int32_t)readlane32((uint32_t)ci, src);
               if (lane == mi) {
                 skey = ek;
                 sv = ev;
