@@ -30,13 +30,20 @@ struct RowState {
   int32_t hist_count;   // ring fill (Sampler.pas:50)
 };
 
-// Top-K stream phase: one record per (row, chunk), two words:
-//   w[0] = tau_key | count << 32   (every logit with key >= tau_key is stored;
-//                                   count may exceed kCandCap: overflow)
-//   w[1] = flags << 32             (flags bit 0: a NaN or +inf logit was seen)
+// Top-K stream phase: one record per (row, chunk):
+//   w    = tau_key | flags << 32  (every logit with key >= tau_key is stored;
+//                                  flags bit 0: a NaN or +inf logit was seen)
+//   n[w] = candidates wave w found (more than its region holds: overflow)
+// The chunk's kCandCap candidate slots are split among the waves that hold
+// logits (wave_cap), so each wave stores without a block-wide count.
 struct ChunkMeta {
-  uint64_t w[2];
+  uint64_t w;
+  uint32_t n[kWaves];
+  uint32_t pad[2];
 };
+__device__ __forceinline__ int wave_cap(int clen) {
+  return clen <= kWaveSpan ? kCandCap : (clen <= 2 * kWaveSpan ? kCandCap / 2 : kCandCap / kWaves);
+}
 
 // A stored candidate: ord_key(value) << 32 | ~index (larger = better, unique).
 typedef uint64_t Cand;
@@ -58,6 +65,9 @@ struct FullMeta {
 // takes the last ticket reads complete records without an L2 writeback or
 // invalidate.
 __device__ __forceinline__ void xstore(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void xstore32(uint32_t *p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ uint64_t xload(const uint64_t *p) {
@@ -204,6 +214,10 @@ __device__ __forceinline__ double wave_incl_scan_f64(double v) {
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
   return __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(wave_incl_scan_f64(v)), 63));
+}
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ uint32_t lane_rank(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();

@@ -220,24 +220,26 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
 // =============================================================================
 // Top-K path (Sampler.pas:327-460).
 //
-// Stream phase (every chunk): each thread keeps 64 logits in registers.  The
-// threshold tau is the largest of 64 sampled thread maxima that at least K
-// thread maxima reach, so >= K logits of the chunk are >= tau and every logit
-// of the chunk's top K is >= tau.  Logits >= tau (about K of them on smooth
-// data) are written as candidates.
+// Stream phase (every 16384-logit chunk): 64 logits per thread in registers;
+// a threshold tau_c that >= Kq logits of the chunk reach (the smallest of the
+// four waves' R-th largest thread maxima); every logit >= tau_c is stored as a
+// candidate key (value, then lower index) in the storing wave's region.
 //
-// Merge phase (last workgroup of the row): candidates >= max(tau) of all
-// chunks are gathered into LDS, filtered once more with a sampled threshold,
-// and rank-sorted by (value desc, index asc).  This is the exact top-K set
-// whenever the K-th value is not tied with a logit outside the set.
+// Merge (the workgroup that takes the row's last ticket): a logit that was
+// not stored is < tau_c <= T = max_c tau_c, so every logit >= T is stored; if
+// at least K are, the row's top K is the K largest of them.  Those keys are
+// compacted into LDS and the top K found by in-wave bitonic sorts and merges.
+// Otherwise (or when a region overflowed) the slower general merge runs: a
+// radix select of theta = the K-th largest stored key, and a re-read of every
+// chunk whose tau_c exceeds theta.  A K-th value tied with a logit outside the
+// set sends the row to the exact replay, as the reference's min-buffer keeps
+// the tied logits that arrived first in its own slot order.
 //
-// Finish: when Top-P < 1 runs, the reference's draw order is the stable
-// descending sort of q; with pairwise-distinct non-zero q and all non-zero q
-// within 2^22 of the largest (so every fp64 sum is exact in any order) the
-// result does not depend on the min-buffer's slot order and the fast path
-// finishes in one wave.  Otherwise the row replays the reference min-buffer
-// exactly (first strict-minimum slot evicted) and finishes in slot order.
+// Finish: see topk_fast and topk_replay.
 // =============================================================================
+constexpr int kMergeSpec = 8;   // candidate slots loaded per thread per round
+constexpr int kMergeTop = 512;  // keys >= T handled by the bitonic merge
+
 struct TopkSmem {
   uint32_t thr[64];
   uint32_t cnt[kWaves][64];
@@ -272,7 +274,7 @@ struct TopkSmem {
   int32_t i_ord[kKMax];
   float v_ord[kKMax];
   uint32_t pbits[kChunk / 32];  // fused penalty: positions of the chunk it changed
-  uint32_t pm, pen_n;
+  uint32_t pm, pen_n, pflag;
   union {
     uint64_t sk[kMergeCap];
     struct {
@@ -295,7 +297,7 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 // or re-reads the chunks for which that fails, so Kq may be far below K: the
 // row's top 64 holds about 64/S logits of each of its S chunks.
 __device__ __forceinline__ int chunk_quota(int K, int S) {
-  if (S <= 1 || S * kCandCap > kMergeCap) return K;
+  if (S <= 1) return K;
   const int q = (3 * K + S - 1) / S + 4;
   return min(K, max(8, q));
 }
@@ -351,6 +353,7 @@ __device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int 
   if (tid == 0) {
     sm.pm = 0u;
     sm.pen_n = 0u;
+    sm.pflag = 0u;
   }
   __syncthreads();
 #pragma unroll
@@ -378,6 +381,7 @@ __device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int 
     if (rep) {
       const float x = penalise(sm.buf.pen.x[e], k, p.penalty);
       xstoref(&L[id], x);
+      if (!(x <= 3.4028235e38f)) sm.pflag = 1u;  // NaN, or +inf (e.g. a boost that overflowed)
       atomicOr(&sm.pbits[(id - c0) >> 5], 1u << ((id - c0) & 31));
       const uint32_t q = atomicAdd(&sm.pen_n, 1u);
       sm.buf.pen.key[q] = ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)id);
@@ -455,47 +459,60 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   }
   const float tf = key_float(tau);
 
-  // Candidates: one wave-wide ballot per float4 group tests the group maxima;
-  // only groups in which some lane passes test their four logits (wave-uniform
-  // branches, so a wave spends ~1 VALU op on each group without candidates).
-  // Positions changed by the fused penalty are skipped here and stored from
-  // its list below.
+  // Candidates: each wave stores into its own region of the chunk's slots
+  // (wave_cap), at a running wave count plus the lane's rank in the ballot,
+  // so no block-wide count or barrier is needed.  Full chunks test one float4
+  // group maximum per compare and branch (wave-uniform) only into groups in
+  // which some lane passes.  Positions changed by the fused penalty are
+  // skipped; their new values are stored from the penalty's list.
   const bool all = (tau == 0u);
-  uint32_t hitj = 0u, wcnt = 0u;  // wave-uniform
-#pragma unroll
-  for (int j = 0; j < kG; ++j) {
-    const int l0 = chunk_pos(wv, lane, 4 * j);
-    const bool gp = (l0 < clen) && (all || gm[j] >= tf);
-    if (__ballot(gp) != 0ull) {
-      hitj |= 1u << j;
-      uint32_t pb = 0u;
-      if (PEN && npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
-        wcnt += (uint32_t)__popcll(__ballot(hit));
+  const int cap = wave_cap(clen);
+  Cand *wreg = cand + wv * cap;
+  uint32_t wc = 0u;  // wave-uniform
+  if (PEN && npen) {
+    for (uint32_t i0 = 0u; i0 < npen; i0 += 64u) {
+      const uint32_t i = i0 + (uint32_t)lane;
+      uint64_t k = 0ull;
+      bool own = false;
+      if (i < npen) {
+        k = sm.buf.pen.key[i];
+        own = ((((int)(~(uint32_t)k)) - c0) >> 12) == wv && (all || (uint32_t)(k >> 32) >= tau);
+      }
+      const uint64_t ob = __ballot(own);
+      if (ob) {
+        const uint32_t q = wc + lane_rank(ob);
+        if (own && q < (uint32_t)cap) xstore(&wreg[q], k);
+        wc += (uint32_t)__popcll(ob);
       }
     }
   }
-  if (lane == 0) sm.wtot[wv] = wcnt;
-  __syncthreads();
-  uint32_t pos = 0u, total = 0u;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    if (w < wv) pos += sm.wtot[w];
-    total += sm.wtot[w];
-  }
-  if (PEN) {
-    for (uint32_t i = tid; i < npen; i += kBlock)  // penalised logits, unconditionally
-      if (total + i < (uint32_t)kCandCap) xstore(&cand[total + i], sm.buf.pen.key[i]);
-    total += npen;
-  }
-  if (hitj) {
+  if (clen == kChunk && !all) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
-      if ((hitj >> j) & 1u) {
+      if (__ballot(gm[j] >= tf)) {
         const int l0 = chunk_pos(wv, lane, 4 * j);
-        const bool gp = (l0 < clen) && (all || gm[j] >= tf);
+        uint32_t pb = 0u;
+        if (PEN && npen) pb = (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool hit = v[4 * j + e] >= tf && !((pb >> e) & 1u);
+          const uint64_t hb = __ballot(hit);
+          if (hb) {
+            const uint32_t q = wc + lane_rank(hb);
+            if (hit && q < (uint32_t)cap)
+              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
+                                   (uint32_t)(~(uint32_t)(c0 + l0 + e)));
+            wc += (uint32_t)__popcll(hb);
+          }
+        }
+      }
+    }
+  } else if (chunk_pos(wv, 0, 0) < clen) {  // short chunk, or tau = 0: test positions too
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      const int l0 = chunk_pos(wv, lane, 4 * j);
+      const bool gp = (l0 < clen) && (all || gm[j] >= tf);
+      if (__ballot(gp)) {
         uint32_t pb = 0u;
         if (PEN && npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
 #pragma unroll
@@ -503,21 +520,21 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
           const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
           const uint64_t hb = __ballot(hit);
           if (hb) {
-            const uint32_t q = pos + __builtin_amdgcn_mbcnt_hi((uint32_t)(hb >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)hb, 0u));
-            if (hit && q < (uint32_t)kCandCap)
-              xstore(&cand[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
+            const uint32_t q = wc + lane_rank(hb);
+            if (hit && q < (uint32_t)cap)
+              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
                                    (uint32_t)(~(uint32_t)(c0 + l0 + e)));
-            pos += (uint32_t)__popcll(hb);
+            wc += (uint32_t)__popcll(hb);
           }
         }
       }
     }
   }
+  if (lane == 0) xstore32(&meta->n[wv], wc);
   if (tid == 0) {
-    const uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
-    xstore(&meta->w[0], (uint64_t)tau | ((uint64_t)total << 32));
-    xstore(&meta->w[1], (uint64_t)fl << 32);
+    uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
+    if (PEN && pen) fl |= sm.pflag;
+    xstore(&meta->w, (uint64_t)tau | ((uint64_t)fl << 32));
   }
 }
 
@@ -588,63 +605,101 @@ __device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, TopkSmem &sm, u
   return prefix;
 }
 
-// Merge phase (last workgroup of the row).  One round trip loads the chunk
-// records and every candidate slot into LDS; a radix select finds theta, the
-// K-th largest stored value.  The stored set holds the row's top K (and every
-// logit tied with theta) when theta >= tau_c for every chunk c, since a logit
-// that was not stored is < tau_c.  Chunks where that fails (or whose store
-// overflowed) are re-read from HBM against theta, a lower bound of the row's
-// K-th value, and theta is recomputed.  Returns false when the row must be
-// replayed: non-finite logits, LDS capacity exceeded, or the K-th value is
-// tied with a logit outside the set.
+// ---- in-wave bitonic network: 64 keys, one per lane, sorted descending --------------
+// Lane exchanges: DPP quad_perm (xor 1, 2), DPP row_ror:8 (xor 8), ds_swizzle in
+// bit mode (xor 4, 16 inside 32-lane halves) and ds_bpermute (xor 32).
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v) {
+  if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (J == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+  else if constexpr (J == 4 || J == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (J << 10));
+  else return (uint32_t)__builtin_amdgcn_ds_bpermute((lane_id() ^ J) << 2, (int)v);
+}
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  return ((uint64_t)xor_lane32<J>((uint32_t)(v >> 32)) << 32) | xor_lane32<J>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t reverse_lanes64(uint64_t v) {
+  const int a = (63 - lane_id()) << 2;
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)(uint32_t)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)(uint32_t)v);
+}
+// One compare-exchange step of the network: blocks of size K sorted in
+// alternating directions (descending where lane & K == 0; all descending at
+// K = 64), partners J lanes apart.
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t x) {
+  const uint64_t y = xor_lane64<J>(x);
+  const int l = lane_id();
+  const bool keep_max = ((l & J) == 0) == ((K >= 64) || ((l & K) == 0));
+  return (keep_max == (x > y)) ? x : y;
+}
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t x) {
+  x = bitonic_step<2, 1>(x);
+  x = bitonic_step<4, 2>(x);  x = bitonic_step<4, 1>(x);
+  x = bitonic_step<8, 4>(x);  x = bitonic_step<8, 2>(x);  x = bitonic_step<8, 1>(x);
+  x = bitonic_step<16, 8>(x); x = bitonic_step<16, 4>(x); x = bitonic_step<16, 2>(x);
+  x = bitonic_step<16, 1>(x);
+  x = bitonic_step<32, 16>(x); x = bitonic_step<32, 8>(x); x = bitonic_step<32, 4>(x);
+  x = bitonic_step<32, 2>(x);  x = bitonic_step<32, 1>(x);
+  x = bitonic_step<64, 32>(x); x = bitonic_step<64, 16>(x); x = bitonic_step<64, 8>(x);
+  x = bitonic_step<64, 4>(x);  x = bitonic_step<64, 2>(x);  x = bitonic_step<64, 1>(x);
+  return x;
+}
+// A bitonic sequence of 64 keys to descending order.
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t x) {
+  x = bitonic_step<64, 32>(x); x = bitonic_step<64, 16>(x); x = bitonic_step<64, 8>(x);
+  x = bitonic_step<64, 4>(x);  x = bitonic_step<64, 2>(x);  x = bitonic_step<64, 1>(x);
+  return x;
+}
+// Top 64 of two descending 64-key lists held by one wave: the lane-wise
+// maximum of a and reversed b is bitonic and holds the 64 largest.
+__device__ __forceinline__ uint64_t wave_top64(uint64_t a, uint64_t b_reversed) {
+  return wave_merge_desc(a > b_reversed ? a : b_reversed);
+}
+
+// Candidate slot i of the row (chunk i / kCandCap) holds a stored key.
+__device__ __forceinline__ bool slot_valid(int i, int V, const TopkSmem &sm) {
+  const int c = i / kCandCap, e = i - c * kCandCap;
+  const int clen = min(kChunk, V - c * kChunk);
+  const int cap = wave_cap(clen);
+  const int w = e / cap, ei = e - w * cap;
+  return (uint32_t)ei < ((sm.ccount[c] >> (8 * w)) & 0xFFu);
+}
+
+// General merge: every stored candidate goes to LDS; theta = the K-th largest
+// (radix select).  The stored set holds the row's top K (and every logit tied
+// with theta) when theta >= tau_c for every chunk, since a logit that was not
+// stored is < tau_c.  Chunks where that fails (or whose region overflowed)
+// are re-read from HBM against theta, a lower bound of the row's K-th value,
+// and theta is recomputed.  Returns false when the row must be replayed: LDS
+// capacity exceeded, or the K-th value tied with a logit outside the set.
 template <bool VEC>
-__device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, int S, int K,
-                           const ChunkMeta *__restrict__ cm, const Cand *__restrict__ cand_row,
-                           TopkSmem &sm) {
+__device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, int V, int S, int K,
+                                                   const Cand *__restrict__ cand_row, TopkSmem &sm,
+                                                   uint64_t (&kk)[kMergeSpec], bool reload) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  constexpr int kSpec = 8;
   const int nslots = S * kCandCap;
   if (tid == 0) sm.n = 0u;
-  uint32_t fl = 0u;
-  for (int c = tid; c < S; c += kBlock) {
-    const uint64_t w0 = xload(&cm[c].w[0]), w1 = xload(&cm[c].w[1]);
-    const uint32_t count = (uint32_t)(w0 >> 32);
-    fl |= (uint32_t)(w1 >> 32);
-    sm.ccount[c] = min(count, (uint32_t)kCandCap);
-    // a chunk is "open" (must be re-read) when its store overflowed
-    sm.ctau[c] = (count > (uint32_t)kCandCap) ? 0xFFFFFFFFu : (uint32_t)w0;
-  }
-  uint64_t kk[kSpec];
-  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-#pragma unroll
-  for (int r = 0; r < kSpec; ++r) {
-    const int i = tid + r * kBlock;
-    kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
-  }
-  fl = wave_or_u32(fl);
-  if (lane == 0) sm.cnt[1][wv] = fl;
   __syncthreads();
-  fl = sm.cnt[1][0] | sm.cnt[1][1] | sm.cnt[1][2] | sm.cnt[1][3];
-  if (fl) return false;
-  for (int base = 0; base < nslots; base += kSpec * kBlock) {
-    if (base > 0) {
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+  for (int base = 0; base < nslots; base += kMergeSpec * kBlock) {
+    if (base > 0 || reload) {
 #pragma unroll
-      for (int r = 0; r < kSpec; ++r) {
+      for (int r = 0; r < kMergeSpec; ++r) {
         const int i = base + tid + r * kBlock;
         kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
       }
     }
 #pragma unroll
-    for (int r = 0; r < kSpec; ++r) {
+    for (int r = 0; r < kMergeSpec; ++r) {
       const int i = base + tid + r * kBlock;
-      if (i < nslots) {
-        const int c = i / kCandCap, e = i - c * kCandCap;
-        if ((uint32_t)e < sm.ccount[c]) {
-          const uint32_t q = atomicAdd(&sm.n, 1u);
-          if (q < (uint32_t)kMergeCap) sm.buf.sk[q] = kk[r];
-          kmin = min(kmin, (uint32_t)(kk[r] >> 32));
-          kmax = max(kmax, (uint32_t)(kk[r] >> 32));
-        }
+      if (i < nslots && slot_valid(i, V, sm)) {
+        const uint32_t q = atomicAdd(&sm.n, 1u);
+        if (q < (uint32_t)kMergeCap) sm.buf.sk[q] = kk[r];
+        kmin = min(kmin, (uint32_t)(kk[r] >> 32));
+        kmax = max(kmax, (uint32_t)(kk[r] >> 32));
       }
     }
   }
@@ -760,6 +815,129 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
   if (tid == 0) sm.ntop = K;
   __syncthreads();
   return true;
+}
+
+
+// Merge (the last workgroup of the row).  One round trip loads the chunk
+// records and, speculatively, the first kMergeSpec * kBlock candidate slots.
+// Rows holding NaN or +inf are replayed.  With T = max_c tau_c: every logit
+// >= T was stored (a logit that was not is < tau_c <= T), so when at least K
+// of the stored keys reach T -- and at most 512, which holds for all but
+// pathological rows -- the top K are the K largest of them: each wave
+// bitonic-sorts 64 (or 2 x 64) of them, and the four sorted lists are merged
+// pairwise.  Otherwise, or when a wave's region overflowed, the general merge
+// runs.  Returns false when the row must be replayed.
+template <bool VEC>
+__device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, int S, int K,
+                                           const ChunkMeta *__restrict__ cm,
+                                           const Cand *__restrict__ cand_row, TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nslots = S * kCandCap;
+  uint32_t fl = 0u, tmx = 0u;
+  for (int c = tid; c < S; c += kBlock) {
+    const uint64_t w0 = xload(&cm[c].w);
+    const uint64_t n01 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[0]));
+    const uint64_t n23 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[2]));
+    const uint32_t cap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk));
+    const uint32_t n0 = (uint32_t)n01, n1 = (uint32_t)(n01 >> 32), n2 = (uint32_t)n23,
+                   n3 = (uint32_t)(n23 >> 32);
+    const bool ovf = n0 > cap || n1 > cap || n2 > cap || n3 > cap;
+    sm.ccount[c] = min(n0, cap) | (min(n1, cap) << 8) | (min(n2, cap) << 16) | (min(n3, cap) << 24);
+    const uint32_t tau = ovf ? 0xFFFFFFFFu : (uint32_t)w0;  // an overflowed chunk is "open"
+    sm.ctau[c] = tau;
+    tmx = max(tmx, tau);
+    fl |= (uint32_t)(w0 >> 32);
+  }
+  uint64_t kk[kMergeSpec];
+#pragma unroll
+  for (int r = 0; r < kMergeSpec; ++r) {
+    const int i = tid + r * kBlock;
+    kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
+  }
+  fl = wave_or_u32(fl);
+  tmx = wave_max_u32(tmx);
+  if (lane == 0) {
+    sm.cnt[1][wv] = fl;
+    sm.cnt[2][wv] = tmx;
+  }
+  __syncthreads();
+  fl = sm.cnt[1][0] | sm.cnt[1][1] | sm.cnt[1][2] | sm.cnt[1][3];
+  tmx = max(max(sm.cnt[2][0], sm.cnt[2][1]), max(sm.cnt[2][2], sm.cnt[2][3]));
+  if (fl) return false;
+  if (tmx == 0xFFFFFFFFu) return topk_merge_general<VEC>(L, V, S, K, cand_row, sm, kk, false);
+
+  // keys >= T, compacted by a block-wide exclusive scan
+  const uint64_t thr = (uint64_t)tmx << 32;
+  uint32_t nf = 0u;
+  for (int base = 0; base < nslots; base += kMergeSpec * kBlock) {
+    if (base > 0) {
+#pragma unroll
+      for (int r = 0; r < kMergeSpec; ++r) {
+        const int i = base + tid + r * kBlock;
+        kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
+      }
+    }
+    uint32_t vb = 0u, m = 0u;
+#pragma unroll
+    for (int r = 0; r < kMergeSpec; ++r) {
+      const int i = base + tid + r * kBlock;
+      const bool ok = i < nslots && kk[r] >= thr && slot_valid(i, V, sm);
+      vb |= ok ? (1u << r) : 0u;
+      m += ok ? 1u : 0u;
+    }
+    const uint32_t incl = wave_incl_scan_u32(m);
+    if (lane == 63) sm.wtot[wv] = incl;
+    __syncthreads();
+    uint32_t off = nf + incl - m, total = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      if (w < wv) off += sm.wtot[w];
+      total += sm.wtot[w];
+    }
+#pragma unroll
+    for (int r = 0; r < kMergeSpec; ++r) {
+      if ((vb >> r) & 1u) {
+        if (off < (uint32_t)kMergeTop) sm.buf.sk[off] = kk[r];
+        ++off;
+      }
+    }
+    nf += total;
+    __syncthreads();
+  }
+  if (nf < (uint32_t)K || nf > (uint32_t)kMergeTop)
+    return topk_merge_general<VEC>(L, V, S, K, cand_row, sm, kk, nslots > kMergeSpec * kBlock);
+
+  // top 64 of the nf <= 512 keys
+  uint64_t *R = sm.buf.sk + kMergeTop;  // four sorted lists of 64
+  const uint32_t i0 = (uint32_t)(wv * 64 + lane);
+  uint64_t a = wave_sort_desc(i0 < nf ? sm.buf.sk[i0] : 0ull);
+  if (nf > 256u) {
+    const uint64_t b = wave_sort_desc(i0 + 256u < nf ? sm.buf.sk[i0 + 256u] : 0ull);
+    a = wave_top64(a, reverse_lanes64(b));
+  }
+  R[i0] = a;
+  __syncthreads();
+  if (wv == 0 || wv == 2) {
+    a = wave_top64(a, R[(wv + 1) * 64 + 63 - lane]);
+    R[i0] = a;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    a = wave_top64(a, R[2 * 64 + 63 - lane]);
+    // The reference keeps the top K; if the K-th value is shared by a stored
+    // key outside them, which tied logits it keeps depends on its slot order.
+    const uint32_t vk = (uint32_t)(readlane64(a, K - 1) >> 32);
+    const uint32_t inset = (uint32_t)__popcll(__ballot(lane < K && (uint32_t)(a >> 32) == vk));
+    uint32_t tied = 0u;
+    for (uint32_t j0 = 0u; j0 < nf; j0 += 64u) {
+      const uint32_t j = j0 + (uint32_t)lane;
+      tied += (uint32_t)__popcll(__ballot(j < nf && (uint32_t)(sm.buf.sk[j] >> 32) == vk));
+    }
+    if (lane < K) sm.topkey[lane] = a;
+    if (lane == 0) sm.ntop = (tied > inset) ? -1 : K;
+  }
+  __syncthreads();
+  return sm.ntop == K;
 }
 
 // Fast finish over the sorted top-K.  With Top-P < 1 the reference draws in
