@@ -67,7 +67,7 @@ WORKLOADS = {
         rows=1, vocab=262144, hist=0, cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3001),
         desc="B=1 V=262144 fp32 3*N(0,1)+8 at 16 ids, T 1.0, top-k 64, top-p 0.95"),
 }
-DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec_pen", "topk_b256": "k_topk_vec",
+DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec"}
 

@@ -6,7 +6,9 @@ travels with the source tree.
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import subprocess
 
 PKG = os.path.dirname(os.path.abspath(__file__))
@@ -33,17 +35,44 @@ HIP_FLAGS = [
 ]
 
 
+RESOURCES = os.path.join(LIBDIR, "kernel_resources.json")
+
+
+def parse_resource_remarks(text: str) -> dict:
+    """Per-kernel register / scratch / occupancy figures from hipcc's
+    -Rpass-analysis=kernel-resource-usage remarks."""
+    out, cur = {}, None
+    fields = {"VGPRs": "vgprs", "TotalSGPRs": "sgprs", "ScratchSize [bytes/lane]": "scratch",
+              "Occupancy [waves/SIMD]": "occupancy", "LDS Size [bytes/block]": "lds",
+              "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill"}
+    for line in text.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([^:]+?): (\S+) \[-Rpass-analysis", line)
+        if m and cur is not None and m.group(1) in fields:
+            v = m.group(2)
+            cur[fields[m.group(1)]] = int(v) if v.isdigit() else v
+    return out
+
+
 def build_library(verbose: bool = False) -> str:
-    """Compiles every source for gfx950; always recompiles."""
+    """Compiles every source for gfx950; always recompiles.  Writes the
+    kernels' resource usage (registers, scratch, occupancy) next to the
+    library."""
     os.makedirs(LIBDIR, exist_ok=True)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp,
+    cmd = [HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage",
+           "-I", os.path.join(ROOT, "include"), "-o", tmp,
            *[os.path.join(CSRC, s) for s in SOURCES]]
     r = subprocess.run(cmd, cwd=CSRC, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + r.stdout + r.stderr)
     if verbose:
         print(" ".join(cmd))
+    with open(RESOURCES, "w") as f:
+        json.dump(parse_resource_remarks(r.stderr), f, indent=1, sort_keys=True)
     os.replace(tmp, LIB)
     return LIB
 

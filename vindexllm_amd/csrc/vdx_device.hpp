@@ -41,8 +41,11 @@ struct ChunkMeta {
   uint32_t n[kWaves];
   uint32_t pad[2];
 };
+// Chunks are read in the interleaved layout (position j*1024 + wave*256 + ...),
+// so a short chunk of <= 256 logits lives in wave 0 and one of <= 512 in waves
+// 0 and 1.
 __device__ __forceinline__ int wave_cap(int clen) {
-  return clen <= kWaveSpan ? kCandCap : (clen <= 2 * kWaveSpan ? kCandCap / 2 : kCandCap / kWaves);
+  return clen <= 256 ? kCandCap : (clen <= 512 ? kCandCap / 2 : kCandCap / kWaves);
 }
 
 // A stored candidate: ord_key(value) << 32 | ~index (larger = better, unique).

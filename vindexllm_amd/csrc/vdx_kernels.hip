@@ -47,16 +47,26 @@ __device__ __forceinline__ double block_excl_scan_f64(double x, double *wtot, do
   return base + (incl - x);
 }
 
-// Loads one chunk: thread (wave wv, lane) owns logits
-//   wv*4096 + j*256 + lane*4 + e,  j < 16, e < 4
-// (each wave reads a contiguous 16 KiB span, 1 KiB per instruction).
+// Chunk layouts.  Thread (wave wv, lane) owns 16 float4 groups j of a chunk:
+//   interleaved (default):  j*1024 + wv*256 + lane*4 + e
+//     the workgroup's j-th load instruction reads one contiguous 4 KiB piece,
+//     which spreads the four waves' requests over HBM channels better than
+//     four pieces 16 KiB apart (measured: ~2 us less per 64 MiB);
+//   span (SPAN = true):     wv*4096 + j*256 + lane*4 + e
+//     each wave owns a contiguous 4096-logit span (the full-softmax path
+//     locates its draw inside one such span).
+template <bool SPAN = false>
+__device__ __forceinline__ int chunk_pos(int wv, int lane, int i) {
+  return SPAN ? wv * kWaveSpan + (i >> 2) * 256 + lane * 4 + (i & 3)
+              : (i >> 2) * 1024 + wv * 256 + lane * 4 + (i & 3);
+}
 // Positions at or beyond `clen` read as `fill`.
-template <bool VEC>
+template <bool VEC, bool SPAN = false>
 __device__ __forceinline__ void load_chunk(const float *__restrict__ base, int clen, int wv,
                                            int lane, float (&v)[kPerThread], float fill) {
 #pragma unroll
   for (int j = 0; j < kPerThread / 4; ++j) {
-    const int local = wv * kWaveSpan + j * 256 + lane * 4;
+    const int local = chunk_pos<SPAN>(wv, lane, 4 * j);
     if (VEC && local + 4 <= clen) {
       const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base + local));
       v[4 * j + 0] = f[0];
@@ -68,9 +78,6 @@ __device__ __forceinline__ void load_chunk(const float *__restrict__ base, int c
       for (int e = 0; e < 4; ++e) v[4 * j + e] = (local + e < clen) ? base[local + e] : fill;
     }
   }
-}
-__device__ __forceinline__ int chunk_pos(int wv, int lane, int i) {
-  return wv * kWaveSpan + (i >> 2) * 256 + lane * 4 + (i & 3);
 }
 
 // Last-workgroup election for a row: returns true in every thread of the
@@ -290,6 +297,10 @@ struct TopkSmem {
 };
 
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// Maximum of float4 group j of a thread's logits (NaN-propagating).
+__device__ __forceinline__ float gmax4(const float (&v)[kPerThread], int j) {
+  return vmax(vmax(vmax(v[4 * j], v[4 * j + 1]), v[4 * j + 2]), v[4 * j + 3]);
+}
 
 // Per-chunk candidate quota.  A chunk stores every logit >= tau_c, where tau_c
 // guarantees >= Kq stored logits.  The merge proves afterwards that the stored
@@ -390,14 +401,14 @@ __device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int 
   __syncthreads();
 }
 
-template <bool VEC, bool PEN>
+template <bool VEC>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
                                             ChunkMeta *__restrict__ meta, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
   PenaltyPrefetch pf;
-  const bool pen = PEN && p.fuse_penalty != 0;
+  const bool pen = p.fuse_penalty != 0;
   if (pen) penalty_prefetch(p, row, pf);
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
@@ -407,13 +418,11 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
-  float gm[kG];
+  // (group maxima are recomputed where they are tested, which keeps 16 fewer
+  // registers live across the threshold search)
+  float m = gmax4(v, 0);
 #pragma unroll
-  for (int j = 0; j < kG; ++j)
-    gm[j] = vmax(vmax(vmax(v[4 * j], v[4 * j + 1]), v[4 * j + 2]), v[4 * j + 3]);
-  float m = gm[0];
-#pragma unroll
-  for (int j = 1; j < kG; ++j) m = vmax(m, gm[j]);
+  for (int j = 1; j < kG; ++j) m = vmax(m, gmax4(v, j));
   const bool hasv = chunk_pos(wv, lane, 0) < clen;
   const bool bad = hasv && !(m <= 3.4028235e38f);
   const uint32_t mk = hasv ? ord_key(m) : 0u;
@@ -469,14 +478,14 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   const int cap = wave_cap(clen);
   Cand *wreg = cand + wv * cap;
   uint32_t wc = 0u;  // wave-uniform
-  if (PEN && npen) {
+  if (npen) {
     for (uint32_t i0 = 0u; i0 < npen; i0 += 64u) {
       const uint32_t i = i0 + (uint32_t)lane;
       uint64_t k = 0ull;
       bool own = false;
       if (i < npen) {
         k = sm.buf.pen.key[i];
-        own = ((((int)(~(uint32_t)k)) - c0) >> 12) == wv && (all || (uint32_t)(k >> 32) >= tau);
+        own = (((((int)(~(uint32_t)k)) - c0) >> 8) & 3) == wv && (all || (uint32_t)(k >> 32) >= tau);
       }
       const uint64_t ob = __ballot(own);
       if (ob) {
@@ -489,10 +498,10 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   if (clen == kChunk && !all) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
-      if (__ballot(gm[j] >= tf)) {
+      if (__ballot(gmax4(v, j) >= tf)) {
         const int l0 = chunk_pos(wv, lane, 4 * j);
         uint32_t pb = 0u;
-        if (PEN && npen) pb = (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu;
+        if (npen) pb = (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool hit = v[4 * j + e] >= tf && !((pb >> e) & 1u);
@@ -511,10 +520,10 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
       const int l0 = chunk_pos(wv, lane, 4 * j);
-      const bool gp = (l0 < clen) && (all || gm[j] >= tf);
+      const bool gp = (l0 < clen) && (all || gmax4(v, j) >= tf);
       if (__ballot(gp)) {
         uint32_t pb = 0u;
-        if (PEN && npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
+        if (npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
@@ -533,7 +542,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   if (lane == 0) xstore32(&meta->n[wv], wc);
   if (tid == 0) {
     uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
-    if (PEN && pen) fl |= sm.pflag;
+    if (pen) fl |= sm.pflag;
     xstore(&meta->w, (uint64_t)tau | ((uint64_t)fl << 32));
   }
 }
@@ -659,13 +668,18 @@ __device__ __forceinline__ uint64_t wave_top64(uint64_t a, uint64_t b_reversed) 
   return wave_merge_desc(a > b_reversed ? a : b_reversed);
 }
 
-// Candidate slot i of the row (chunk i / kCandCap) holds a stored key.
-__device__ __forceinline__ bool slot_valid(int i, int V, const TopkSmem &sm) {
+// Candidate slot i of the row (chunk i / kCandCap) holds a stored key.  Only
+// the row's last chunk can be short, so every other chunk has regions of
+// kCandCap / kWaves slots; `last_sh` is log2 of the last chunk's region size.
+__device__ __forceinline__ bool slot_valid(int i, int S, int last_sh, const TopkSmem &sm) {
   const int c = i / kCandCap, e = i - c * kCandCap;
-  const int clen = min(kChunk, V - c * kChunk);
-  const int cap = wave_cap(clen);
-  const int w = e / cap, ei = e - w * cap;
-  return (uint32_t)ei < ((sm.ccount[c] >> (8 * w)) & 0xFFu);
+  const int sh = (c == S - 1) ? last_sh : 5;
+  static_assert(kCandCap / kWaves == 32, "full-chunk regions hold 32 slots");
+  return (uint32_t)(e & ((1 << sh) - 1)) < ((sm.ccount[c] >> (8 * (e >> sh))) & 0xFFu);
+}
+__device__ __forceinline__ int last_region_sh(int V, int S) {
+  const int cap = wave_cap(V - (S - 1) * kChunk);
+  return cap == 128 ? 7 : (cap == 64 ? 6 : 5);
 }
 
 // General merge: every stored candidate goes to LDS; theta = the K-th largest
@@ -681,6 +695,7 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
                                                    uint64_t (&kk)[kMergeSpec], bool reload) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslots = S * kCandCap;
+  const int last_sh = last_region_sh(V, S);
   if (tid == 0) sm.n = 0u;
   __syncthreads();
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
@@ -695,7 +710,7 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
 #pragma unroll
     for (int r = 0; r < kMergeSpec; ++r) {
       const int i = base + tid + r * kBlock;
-      if (i < nslots && slot_valid(i, V, sm)) {
+      if (i < nslots && slot_valid(i, S, last_sh, sm)) {
         const uint32_t q = atomicAdd(&sm.n, 1u);
         if (q < (uint32_t)kMergeCap) sm.buf.sk[q] = kk[r];
         kmin = min(kmin, (uint32_t)(kk[r] >> 32));
@@ -868,6 +883,7 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
 
   // keys >= T, compacted by a block-wide exclusive scan
   const uint64_t thr = (uint64_t)tmx << 32;
+  const int last_sh = last_region_sh(V, S);
   uint32_t nf = 0u;
   for (int base = 0; base < nslots; base += kMergeSpec * kBlock) {
     if (base > 0) {
@@ -881,7 +897,7 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
 #pragma unroll
     for (int r = 0; r < kMergeSpec; ++r) {
       const int i = base + tid + r * kBlock;
-      const bool ok = i < nslots && kk[r] >= thr && slot_valid(i, V, sm);
+      const bool ok = i < nslots && kk[r] >= thr && slot_valid(i, S, last_sh, sm);
       vb |= ok ? (1u << r) : 0u;
       m += ok ? 1u : 0u;
     }
@@ -972,14 +988,14 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
         const float thr = qmax * p.min_p;
         if (q < thr) q = 0.0f;
       }
-      const double S = wave_sum_f64((double)q);
-      const double target = (double)p.top_p * S;
       const double incl = wave_incl_scan_f64((double)q);
+      const double S = __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(incl), 63));
+      const double target = (double)p.top_p * S;
       const bool kept = act && ((incl - (double)q) < target) && q > 0.0f;  // Top-P (:431-444)
       const float qk = kept ? q : 0.0f;
-      const double S2 = wave_sum_f64((double)qk);
-      const double t = (double)sm.uval * S2;  // draw (:447-459)
       const double c2 = wave_incl_scan_f64((double)qk);
+      const double S2 = __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(c2), 63));
+      const double t = (double)sm.uval * S2;  // draw (:447-459)
       const uint64_t hit = __ballot(act && c2 > t);
       const int pos = hit ? (__ffsll((unsigned long long)hit) - 1) : -1;
       const uint64_t dropm = __ballot(act && !kept);
@@ -1324,7 +1340,7 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
   }
 }
 
-template <bool VEC, bool PEN>
+template <bool VEC>
 __device__ __forceinline__ void topk_body(const CallParams &p) {
   __shared__ TopkSmem sm;
   int row, chunk;
@@ -1335,7 +1351,7 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
-  topk_stream<VEC, PEN>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
+  topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
                         cm + chunk, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
   if (threadIdx.x == 0) {
@@ -1352,9 +1368,8 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
 }
 
 // 16-byte aligned rows: four workgroups per CU (<= 128 VGPRs, no spills).
-__global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true, false>(p); }
-__global__ __launch_bounds__(kBlock, 4) void k_topk_vec_pen(CallParams p) { topk_body<true, true>(p); }
-__global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_body<false, true>(p); }
+__global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_body<false>(p); }
 
 // =============================================================================
 // Full-softmax path (Sampler.pas:461-527): s = fl32(L*invT), M = max s,
@@ -1434,14 +1449,14 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   const int c0 = chunk * kChunk;
   const int clen = min(kChunk, V - c0);
   float v[kPerThread];
-  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  load_chunk<VEC, true>(L + c0, clen, wv, lane, v, -INFINITY);
 
   // s = fl32(L * invT); positions past the row end weigh nothing
   float m = -INFINITY;
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
-    if (chunk_pos(wv, lane, i) < clen) {
+    if (chunk_pos<true>(wv, lane, i) < clen) {
       v[i] = v[i] * p.inv_t;
       m = fmaxf(m, v[i]);
       bad = bad || (v[i] != v[i]);
@@ -1700,9 +1715,7 @@ hipError_t launch_greedy(const CallParams &p, hipStream_t st) {
 }
 
 hipError_t launch_topk(const CallParams &p, hipStream_t st) {
-  if (p.vec && p.fuse_penalty)
-    hipLaunchKernelGGL(k_topk_vec_pen, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
-  else if (p.vec)
+  if (p.vec)
     hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
   else
     hipLaunchKernelGGL(k_topk_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
