@@ -106,6 +106,31 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows,
                                const float *uniforms,
                                const vdx_sample_outputs *out, void *stream);
 
+/* The Q4_0 lm_head alone: shaders/matvec_q4_0.comp as
+ * TVdxAttention.DispatchMatVec issues it for ATensorType = gtQ4_0
+ * (Attention.pas:979-1025) from TVdxModel.UnembedToLogits (Model.pas:1258-1270),
+ * batched over `rows` hidden vectors:
+ *   logits[r*logit_stride + v] = sum_e dequant(W[v][e]) * hidden[r*in_dim + e].
+ * `weights`: vocab rows of in_dim/32 Q4_0 blocks (18 bytes: fp16 scale, then
+ * 16 bytes of nibbles; GGUFReader.pas:264-281), 16-byte aligned; in_dim must
+ * be a multiple of 256.  Every pointer is device memory.  Stream-ordered,
+ * asynchronous, allocates nothing; the message of a failure is
+ * vdx_sampler_last_error(NULL). */
+int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
+                    int32_t vocab, float *logits, int64_t logit_stride, void *stream);
+
+/* RunUnembedding followed by Process (Inference.pas:327-339) with the logits
+ * kept in HBM: the Q4_0 lm_head (as vdx_lmhead_q4_0) writes rows x vocab
+ * logits into `logits` (device, row stride logit_stride >= vocab) or, when
+ * `logits` is NULL, into the sampler's own workspace (allocated on the first
+ * call with a larger rows*vocab); the rows are then sampled exactly as by
+ * vdx_sampler_process_device (penalty in place, per-row RNG or injected
+ * uniforms, same outputs). */
+int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const float *hidden,
+                                   int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
+                                   int64_t logit_stride, const float *uniforms,
+                                   const vdx_sample_outputs *out, void *stream);
+
 /* TVdxSampler.AddToHistory (Sampler.pas:530-539) for one row. */
 int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token);
 

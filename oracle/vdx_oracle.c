@@ -578,3 +578,70 @@ void vdxo_matvec_q4_0(const uint8_t *w, const float *x, int32_t in_dim,
     logits[r] = partial[0];
   }
 }
+
+/* The same matvec in the accumulation order of the library's fused lm_head
+ * kernel (not the shader's): per row, blocks k = 0.. in order, s = 0,
+ * s = fmaf(q_i - 8, x[32k+i], s) for i = 0..31 (element order: low nibbles
+ * of qs[0..15], then high nibbles), acc = fmaf(d_k, s, acc).  Mathematically
+ * the same sum as matvec_q4_0.comp:57-83; only the fp32 rounding points
+ * differ (the shader's own are unpinned under GLSL contraction). */
+void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
+                              int32_t rows, float *logits) {
+  const int32_t bpr = in_dim >> 5;
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint8_t *row = w + (int64_t)r * bpr * 18;
+    float acc = 0.0f;
+    for (int32_t k = 0; k < bpr; ++k) {
+      const uint8_t *b = row + (int64_t)k * 18;
+      const float d = vdxo_half_to_float((uint16_t)(b[0] | (b[1] << 8)));
+      float s = 0.0f;
+      for (int32_t i = 0; i < 32; ++i) {
+        const uint32_t raw = b[2 + (i & 15)];
+        const int32_t q = (int32_t)((raw >> ((i >> 4) * 4)) & 0xFu) - 8;
+        s = fmaf((float)q, x[32 * k + i], s);
+      }
+      acc = fmaf(d, s, acc);
+    }
+    logits[r] = acc;
+  }
+}
+
+typedef struct {
+  const uint8_t *w;
+  const float *x;
+  int32_t in_dim, r0, r1, blocked;
+  float *out;
+} mv_job;
+
+static void *mv_worker(void *arg) {
+  const mv_job *j = (const mv_job *)arg;
+  const int64_t rb = (int64_t)(j->in_dim >> 5) * 18;
+  if (j->r1 > j->r0) {
+    if (j->blocked)
+      vdxo_matvec_q4_0_blocked(j->w + rb * j->r0, j->x, j->in_dim, j->r1 - j->r0, j->out + j->r0);
+    else
+      vdxo_matvec_q4_0(j->w + rb * j->r0, j->x, j->in_dim, j->r1 - j->r0, j->out + j->r0);
+  }
+  return NULL;
+}
+
+void vdxo_matvec_q4_0_mt(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                         float *logits, int32_t blocked, int32_t threads) {
+  if (threads < 1) threads = 1;
+  pthread_t *tid = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+  mv_job *jobs = (mv_job *)malloc(sizeof(mv_job) * (size_t)threads);
+  for (int32_t t = 0; t < threads; ++t) {
+    mv_job *j = &jobs[t];
+    j->w = w;
+    j->x = x;
+    j->in_dim = in_dim;
+    j->r0 = (int32_t)((int64_t)rows * t / threads);
+    j->r1 = (int32_t)((int64_t)rows * (t + 1) / threads);
+    j->blocked = blocked;
+    j->out = logits;
+    pthread_create(&tid[t], NULL, mv_worker, j);
+  }
+  for (int32_t t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+  free(tid);
+  free(jobs);
+}

@@ -135,6 +135,15 @@ void vdxo_sampler_rng_state(const vdxo_sampler *s, uint64_t st[4]);
  * 32..1).  `w` holds rows x (in_dim/32) blocks of 18 bytes. */
 void vdxo_matvec_q4_0(const uint8_t *w, const float *x, int32_t in_dim,
                       int32_t rows, float *logits);
+/* The same products summed in the library kernel's order: per row, per
+ * block k in order: s = 0; s = fmaf(q_i - 8, x[32k+i], s) for i = 0..31;
+ * acc = fmaf(d_k, s, acc). */
+void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
+                              int32_t rows, float *logits);
+/* Either order (blocked != 0: the kernel's) over `threads` POSIX threads,
+ * rows split evenly. */
+void vdxo_matvec_q4_0_mt(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                         float *logits, int32_t blocked, int32_t threads);
 /* fp16 -> fp32 (IEEE binary16), as unpackHalf2x16. */
 float vdxo_half_to_float(uint16_t h);
 

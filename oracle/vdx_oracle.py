@@ -108,6 +108,10 @@ def lib():
         L.vdxo_sampler_history.restype = C.c_int32
         L.vdxo_sampler_rng_state.argtypes = [C.c_void_p, P(C.c_uint64)]
         L.vdxo_matvec_q4_0.argtypes = [P(C.c_uint8), P(C.c_float), C.c_int32, C.c_int32, P(C.c_float)]
+        L.vdxo_matvec_q4_0_blocked.argtypes = [P(C.c_uint8), P(C.c_float), C.c_int32, C.c_int32,
+                                               P(C.c_float)]
+        L.vdxo_matvec_q4_0_mt.argtypes = [P(C.c_uint8), P(C.c_float), C.c_int32, C.c_int32,
+                                          P(C.c_float), C.c_int32, C.c_int32]
         L.vdxo_half_to_float.argtypes = [C.c_uint16]
         L.vdxo_half_to_float.restype = C.c_float
         _lib = L
@@ -206,6 +210,26 @@ def matvec_q4_0(w: np.ndarray, x: np.ndarray, in_dim: int, rows: int) -> np.ndar
     w = np.ascontiguousarray(w, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32)
     lib().vdxo_matvec_q4_0(w.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(x), in_dim, rows, _fp(out))
+    return out
+
+
+def matvec_q4_0_blocked(w: np.ndarray, x: np.ndarray, in_dim: int, rows: int) -> np.ndarray:
+    out = np.zeros(rows, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().vdxo_matvec_q4_0_blocked(w.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(x), in_dim, rows,
+                                   _fp(out))
+    return out
+
+
+def matvec_q4_0_mt(w: np.ndarray, x: np.ndarray, in_dim: int, rows: int, blocked: bool,
+                   threads: int = 8) -> np.ndarray:
+    """Either summation order over `threads` host threads (x is one hidden vector)."""
+    out = np.zeros(rows, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().vdxo_matvec_q4_0_mt(w.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(x), in_dim, rows,
+                              _fp(out), 1 if blocked else 0, int(threads))
     return out
 
 

@@ -90,3 +90,23 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(sampler, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         sampler.load_library()
+
+
+def test_lmhead_argument_errors_need_no_gpu():
+    # argument validation runs before any HIP call and reports through
+    # vdx_sampler_last_error(NULL)
+    L = _lib()
+    buf = (C.c_uint8 * 64)()
+    base = C.addressof(buf)
+    al = (base + 15) & ~15
+    hid = C.c_void_p(al)
+    cases = [
+        (C.c_void_p(al), hid, 1, 100, 1024, "multiple of 256"),   # in_dim
+        (C.c_void_p(al + 4), hid, 1, 256, 1024, "aligned"),       # weights alignment
+        (None, hid, 1, 256, 1024, "required"),                    # weights
+        (C.c_void_p(al), hid, 0, 256, 1024, "rows > 0"),          # rows
+    ]
+    for w, h, rows, d, v, msg in cases:
+        rc = L.vdx_lmhead_q4_0(w, h, rows, d, v, C.c_void_p(al), v, None)
+        assert rc == -1
+        assert msg in L.vdx_sampler_last_error(None).decode()

@@ -1,0 +1,193 @@
+"""GPU parity of the Q4_0 lm_head (the reference's shaders/matvec_q4_0.comp,
+dispatched from TVdxModel.UnembedToLogits, src/VindexLLM.Model.pas:1258-1270)
+and of lm_head + sampling with the logits kept in HBM (Gemma-3-4B tied head:
+262144 x 2560 Q4_0, nibbles uniform 0..15, fp16 scales |N(0, 0.02)|, hidden
+rows N(0, 1)).
+
+Bar:
+  * logits bit-exact against the oracle's restatement of the kernel's
+    summation order (oracle/vdx_oracle.c: vdxo_matvec_q4_0_blocked), and within
+    the fp32 summation bound of the shader-order restatement;
+  * sampling on those logits at the sampler's own bar (tokens, top-K sets and
+    order bit-exact, probabilities within 1e-5 relative);
+  * end to end against the shader-order logits followed by the oracle
+    sampler: the same token except where the two fp32 summation orders can
+    flip a decision (a top-K boundary gap or a CDF boundary within the logit
+    error), counted and printed.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import npref
+from gpu_common import compare, log, oracle_rows, u_stream
+from oracle import vdx_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+THREADS = max(1, min(16, os.cpu_count() or 1))
+U = 2.0 ** -24
+
+
+def rand_q4_0(rng, rows, in_dim):
+    nb = in_dim // 32
+    blk = rng.integers(0, 256, (rows, nb, 18), dtype=np.uint8)
+    d = np.abs(rng.standard_normal((rows, nb)) * 0.02).astype(np.float16)
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    return blk.reshape(-1)
+
+
+def magnitude(w, x, in_dim, rows):
+    """sum_e |dequant(W[v][e]) * x[e]| per row (the summation error scale)."""
+    W = np.abs(npref.q4_0_dequant(w, in_dim, rows).astype(np.float64))
+    return W @ np.abs(x.astype(np.float64))
+
+
+def gpu_lmhead(w, H, V, D):
+    import torch
+
+    from vindexllm_amd import lmhead_q4_0
+
+    dev = torch.device("cuda:0")
+    wd = torch.from_numpy(w).to(dev)
+    hd = torch.from_numpy(np.ascontiguousarray(H)).to(dev)
+    out = lmhead_q4_0(wd, hd, V)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("V,D,B", [(4096 + 77, 256, 1), (4096 + 77, 256, 2), (4096 + 77, 256, 3),
+                                   (4096 + 77, 512, 5), (2048, 256, 8), (4096 + 77, 256, 16),
+                                   (1000, 256, 17), (1000, 2560, 4), (300, 2560, 1)])
+def test_lmhead_logits_bit_exact(V, D, B):
+    log(f"[case] lm_head V={V} D={D} B={B}")
+    rng = np.random.default_rng(5000 + V + D + B)
+    w = rand_q4_0(rng, V, D)
+    H = rng.standard_normal((B, D)).astype(np.float32)
+    G = gpu_lmhead(w, H, V, D)
+    mag = None
+    for b in range(B):
+        want = O.matvec_q4_0_blocked(w, H[b], D, V)
+        assert np.array_equal(G[b].view(np.uint32), want.view(np.uint32)), \
+            f"row {b}: {np.flatnonzero(G[b] != want)[:5]}"
+        shader = O.matvec_q4_0(w, H[b], D, V).astype(np.float64)
+        if mag is None or B > 1:
+            mag = magnitude(w, H[b], D, V)
+        assert (np.abs(G[b] - shader) <= 2 * (D // 32 + 40) * U * mag).all()
+    log(f"[done] lm_head V={V} D={D} B={B}")
+
+
+def test_lmhead_special_values():
+    # zero hidden rows, zero scales, a single non-zero element: exact results
+    V, D, B = 512, 256, 3
+    rng = np.random.default_rng(77)
+    w = rand_q4_0(rng, V, D)
+    wb = w.reshape(V, D // 32, 18)
+    wb[7, :, 0:2] = 0  # row 7: scale 0 everywhere
+    H = np.zeros((B, D), dtype=np.float32)
+    H[1, 37] = 1.0
+    H[2] = rng.standard_normal(D).astype(np.float32)
+    G = gpu_lmhead(w, H, V, D)
+    assert (G[0] == 0).all()
+    deq = npref.q4_0_dequant(w, D, V)
+    assert np.array_equal(G[1], deq[:, 37])
+    assert G[2][7] == 0.0
+    for b in range(B):
+        assert np.array_equal(G[b], O.matvec_q4_0_blocked(w, H[b], D, V))
+
+
+def _cfg5(B, seed):
+    rng = np.random.default_rng(seed)
+    V, D = 262144, 2560
+    w = rand_q4_0(rng, V, D)
+    H = rng.standard_normal((B, D)).astype(np.float32)
+    u = u_stream(np.random.default_rng(seed + 1000), B)
+    return w, H, u, V, D
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_cfg5_lmhead_plus_sampling(B):
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    log(f"[case] C5 lm_head + top-k64/top-p0.95/T1 B={B}")
+    w, H, u, V, D = _cfg5(B, 1005 + B)
+    cfg = dict(temperature=1.0, top_k=64, top_p=0.95)
+    dev = torch.device("cuda:0")
+    wd = torch.from_numpy(w).to(dev)
+    hd = torch.from_numpy(H).to(dev)
+    L = torch.empty(B, V, dtype=torch.float32, device=dev)
+    ti = torch.full((B, 64), -1, dtype=torch.int32, device=dev)
+    tp = torch.full((B, 64), -1.0, dtype=torch.float32, device=dev)
+    fl = torch.zeros(B, dtype=torch.int32, device=dev)
+    with TVdxSampler(0, B) as s:
+        c = s.DefaultConfig()
+        c.Temperature, c.TopK, c.TopP = 1.0, 64, 0.95
+        s.SetConfig(c)
+        ud = torch.from_numpy(u).to(dev)
+        tok = s.lmhead_q4_0_device(wd, hd, V, logits=L, uniforms=ud, topk_idx=ti, topk_prob=tp,
+                                   flags=fl)
+        tok2 = s.lmhead_q4_0_device(wd, hd, V, uniforms=ud)  # the sampler's own workspace
+        torch.cuda.synchronize()
+    Lg = L.cpu().numpy()
+    g = dict(tokens=tok.cpu().numpy(), topk_idx=ti.cpu().numpy(), topk_prob=tp.cpu().numpy(),
+             flags=fl.cpu().numpy(), logits_after=Lg)
+    assert np.array_equal(g["tokens"], tok2.cpu().numpy())
+    # logits: bit-exact with the kernel-order restatement
+    for b in range(B):
+        want = O.matvec_q4_0_mt(w, H[b], D, V, True, THREADS)
+        assert np.array_equal(Lg[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    # sampling on the GPU's logits: the sampler's bar
+    orc = oracle_rows(Lg, cfg, u)
+    nb = compare(g, orc, cfg, check_logits=False, label=f"C5 B={B}")
+    # end to end against the shader's summation order
+    flips = 0
+    for b in range(B):
+        Ls = O.matvec_q4_0_mt(w, H[b], D, V, False, THREADS)
+        err = float(np.abs(Ls.astype(np.float64) - Lg[b]).max())
+        tok_s, tr_s = O.process_row(Ls.copy(), O.make_config(**cfg), float(u[b]), trace=True)
+        if tok_s != g["tokens"][b]:
+            srt = np.sort(Ls)[::-1]
+            gap = float(srt[63] - srt[64])
+            tr_g = orc[b][1]
+            bd = min(tr_g.target - tr_g.cdf_lo, tr_g.cdf_hi - tr_g.target) / tr_g.sum_final
+            log(f"  row {b}: shader-order token {tok_s} vs {g['tokens'][b]} "
+                f"(logit err {err:.2e}, K-boundary gap {gap:.2e}, CDF distance {bd:.2e})")
+            assert gap <= 4 * err or bd <= 1e-4, f"row {b}: unexplained token difference"
+            flips += 1
+    log(f"[done] C5 B={B}: near-boundary draws {nb}, shader-order flips {flips}/{B}, "
+        f"flags {sorted(set(g['flags'].tolist()))}")
+
+
+def test_lmhead_greedy_and_penalty():
+    # greedy over lm_head logits is the first index of the maximum; with a
+    # repetition penalty the workspace logits are penalised in place first
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    V, D, B = 50000, 512, 4
+    rng = np.random.default_rng(31)
+    w = rand_q4_0(rng, V, D)
+    H = rng.standard_normal((B, D)).astype(np.float32)
+    hist = rng.integers(0, V, (B, 40)).astype(np.int32)
+    dev = torch.device("cuda:0")
+    wd = torch.from_numpy(w).to(dev)
+    hd = torch.from_numpy(H).to(dev)
+    L = torch.empty(B, V, dtype=torch.float32, device=dev)
+    with TVdxSampler(0, B) as s:
+        c = s.DefaultConfig()
+        c.Temperature, c.RepeatPenalty, c.RepeatWindow = 0.0, 1.3, 64
+        s.SetConfig(c)
+        for r in range(B):
+            s.set_history(r, hist[r])
+        tok = s.lmhead_q4_0_device(wd, hd, V, logits=L).cpu().numpy()
+        torch.cuda.synchronize()
+    Lp = L.cpu().numpy()
+    for b in range(B):
+        raw = O.matvec_q4_0_blocked(w, H[b], D, V)
+        pen = npref.penalty(raw, hist[b], 1.3)
+        assert np.array_equal(Lp[b].view(np.uint32), pen.view(np.uint32))
+        assert tok[b] == int(np.argmax(pen))

@@ -401,3 +401,68 @@ def test_q4_0_matvec_against_dequant():
         part[:, :s] = (part[:, :s] + part[:, s:2 * s]).astype(np.float32)
         s //= 2
     assert np.array_equal(got, part[:, 0])
+
+
+def _exact_q4_0(rng, rows, in_dim):
+    """Q4_0 rows whose scales are 2^-4 or 2^-3 and hidden values multiples of
+    2^-3 in [-4, 4): every product and partial sum is an exact fp32 value, so
+    any summation order gives the exact (float64) result."""
+    nb = in_dim // 32
+    blk = np.zeros((rows, nb, 18), dtype=np.uint8)
+    d = np.where(rng.random((rows, nb)) < 0.5, 2.0 ** -4, 2.0 ** -3).astype(np.float16)
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    blk[:, :, 2:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)
+    x = (rng.integers(-32, 32, in_dim) / 8.0).astype(np.float32)
+    return blk.reshape(-1), x
+
+
+def test_q4_0_both_orders_exact_on_exact_inputs():
+    # closed form: both restatements (the shader's order and the kernel's
+    # blocked order) equal the exact dot product of the dequantised rows
+    rng = np.random.default_rng(21)
+    for in_dim in (256, 2560):
+        rows = 40
+        w, x = _exact_q4_0(rng, rows, in_dim)
+        want = npref.q4_0_dequant(w, in_dim, rows).astype(np.float64) @ x.astype(np.float64)
+        assert np.array_equal(O.matvec_q4_0(w, x, in_dim, rows).astype(np.float64), want)
+        assert np.array_equal(O.matvec_q4_0_blocked(w, x, in_dim, rows).astype(np.float64), want)
+        assert np.array_equal(O.matvec_q4_0_mt(w, x, in_dim, rows, True, 3).astype(np.float64), want)
+        assert np.array_equal(O.matvec_q4_0_mt(w, x, in_dim, rows, False, 3).astype(np.float64), want)
+
+
+def test_q4_0_blocked_nibble_order_is_pinned():
+    # a single non-zero nibble at each element position in turn: only the
+    # documented element order (low nibbles of qs[0..15], then high nibbles)
+    # reproduces x[e] * (q - 8) * d at position e
+    in_dim, rows = 256, 1
+    x = (np.arange(in_dim) + 1).astype(np.float32)
+    for e in (0, 5, 15, 16, 17, 31, 32, 47, 200):
+        blk = np.zeros((in_dim // 32, 18), dtype=np.uint8)
+        blk[:, 0:2] = np.array([1.0], dtype=np.float16).view(np.uint8)
+        blk[:, 2:] = 0x88  # q = 8 everywhere: weight 0
+        k, i = divmod(e, 32)
+        b = blk[k, 2 + (i & 15)]
+        blk[k, 2 + (i & 15)] = (b & 0xF0) | 0x0B if i < 16 else (b & 0x0F) | 0xB0  # q = 11: weight 3
+        got = O.matvec_q4_0_blocked(blk.reshape(-1), x, in_dim, rows)[0]
+        assert got == np.float32(3.0 * (e + 1)), (e, got)
+        assert O.matvec_q4_0(blk.reshape(-1), x, in_dim, rows)[0] == got
+
+
+def test_q4_0_blocked_within_fp32_error_bound():
+    # realistic inputs (config 5: scales |N(0, 0.02)|, hidden N(0,1)): the
+    # blocked order and the shader's order each stay within the standard
+    # summation bound of the exact (float64) result
+    rng = np.random.default_rng(22)
+    rows, in_dim = 256, 2560
+    w = _rand_q4_0(rng, rows, in_dim)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    W = npref.q4_0_dequant(w, in_dim, rows).astype(np.float64)
+    exact = W @ x.astype(np.float64)
+    mag = np.abs(W) @ np.abs(x.astype(np.float64))
+    u = 2.0 ** -24
+    blocked = O.matvec_q4_0_blocked(w, x, in_dim, rows).astype(np.float64)
+    shader = O.matvec_q4_0(w, x, in_dim, rows).astype(np.float64)
+    assert (np.abs(blocked - exact) <= (32 + in_dim // 32 + 1) * u * mag).all()
+    assert (np.abs(shader - exact) <= (in_dim // 64 + 6 + 1) * u * mag).all()
+    # the two orders agree far inside the bound on typical rows
+    assert np.median(np.abs(blocked - shader) / mag) < 1e-7

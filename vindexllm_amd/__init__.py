@@ -5,4 +5,4 @@ The product is libvdxsampler.so (HIP kernels + C ABI, include/vdx_sampler.h);
 """
 from .sampler import (ROW_FALLBACK, ROW_FULL, ROW_GREEDY, ROW_NAN, ROW_TOPK_FAST,  # noqa: F401
                       ROW_TOPK_REPLAY, VDX_RNG_PHILOX, VDX_RNG_XOSHIRO, TVdxSampler,
-                      TVdxSamplerConfig, VdxSamplerError, load_library, version)
+                      TVdxSamplerConfig, VdxSamplerError, lmhead_q4_0, load_library, version)

@@ -35,6 +35,9 @@ struct vdx_sampler {
   FullMeta *d_fmeta = nullptr;
   uint64_t *d_gpart = nullptr;
   uint32_t *d_tickets = nullptr;
+  // lm_head logits workspace (rows x vocab, row stride lm_stride)
+  float *d_lm = nullptr;
+  size_t lm_cap = 0;  // floats
   // host-pointer Process
   float *d_row = nullptr;
   int32_t row_cap = 0;
@@ -49,6 +52,7 @@ struct vdx_sampler {
 constexpr int32_t kTimedCalls = 4096;
 
 static std::string g_create_err;
+static thread_local std::string g_call_err;  // sampler-less entry points
 
 static int fail(vdx_sampler *s, int code, const std::string &msg) {
   if (s) s->err = msg;
@@ -140,7 +144,8 @@ void vdx_sampler_default_config(vdx_sampler_config *c) {
 }
 
 const char *vdx_sampler_last_error(const vdx_sampler *s) {
-  return s ? s->err.c_str() : g_create_err.c_str();
+  if (s) return s->err.c_str();
+  return g_call_err.empty() ? g_create_err.c_str() : g_call_err.c_str();
 }
 
 void vdx_sampler_destroy(vdx_sampler *s) {
@@ -157,6 +162,7 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_gpart);
   (void)hipFree(s->d_tickets);
   (void)hipFree(s->d_row);
+  (void)hipFree(s->d_lm);
   (void)hipFree(s->d_tok);
   for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
   if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -380,6 +386,68 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
                               hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(s, hipStreamSynchronize(s->stream));
   return tok;
+}
+
+static const char *lmhead_check(const void *weights, const float *hidden, int32_t rows,
+                                int32_t in_dim, int32_t vocab) {
+  if (!weights || !hidden) return "lm_head: weights and hidden are required";
+  if (rows <= 0 || vocab <= 0) return "lm_head: need rows > 0 and vocab > 0";
+  if (in_dim <= 0 || in_dim % 256 != 0) return "lm_head: in_dim must be a positive multiple of 256";
+  if ((uintptr_t)weights % 16 != 0) return "lm_head: weights must be 16-byte aligned";
+  if ((int64_t)(in_dim / 32) * 18 * 256 > (int64_t)0x7FFFFFFF) return "lm_head: in_dim too large";
+  return nullptr;
+}
+
+int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
+                    int32_t vocab, float *logits, int64_t logit_stride, void *stream) {
+  if (const char *m = lmhead_check(weights, hidden, rows, in_dim, vocab)) {
+    g_call_err = m;
+    return VDX_E_INVALID_ARG;
+  }
+  if (!logits || logit_stride < vocab) {
+    g_call_err = "lm_head: logits required, logit_stride >= vocab";
+    return VDX_E_INVALID_ARG;
+  }
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride, rows, in_dim, vocab};
+  const hipError_t e = launch_lmhead_q4_0(lp, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    g_call_err = std::string("lm_head launch: ") + hipGetErrorString(e);
+    return VDX_E_HIP;
+  }
+  g_call_err.clear();
+  return VDX_OK;
+}
+
+int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const float *hidden,
+                                   int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
+                                   int64_t logit_stride, const float *uniforms,
+                                   const vdx_sample_outputs *out, void *stream) {
+  if (!s) return VDX_E_INVALID_ARG;
+  if (const char *m = lmhead_check(weights, hidden, rows, in_dim, vocab))
+    return fail(s, VDX_E_INVALID_ARG, m);
+  if (rows > s->max_rows) return fail(s, VDX_E_INVALID_ARG, "lm_head: rows must be <= max_rows");
+  if (!out || !out->tokens) return fail(s, VDX_E_INVALID_ARG, "lm_head: out->tokens is required");
+  HIP_TRY(s, hipSetDevice(s->device));
+  int64_t ls = logit_stride;
+  if (!logits) {
+    ls = ((int64_t)vocab + 3) & ~(int64_t)3;  // 16-byte aligned rows
+    const size_t need = (size_t)rows * (size_t)ls;
+    if (need > s->lm_cap) {
+      HIP_TRY(s, hipStreamSynchronize(s->stream));
+      HIP_TRY(s, hipDeviceSynchronize());
+      (void)hipFree(s->d_lm);
+      s->d_lm = nullptr;
+      s->lm_cap = 0;
+      HIP_TRY(s, hipMalloc(&s->d_lm, need * sizeof(float)));
+      s->lm_cap = need;
+    }
+    logits = s->d_lm;
+  } else if (ls < vocab) {
+    return fail(s, VDX_E_INVALID_ARG, "lm_head: logit_stride must be >= vocab");
+  }
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab};
+  HIP_TRY(s, launch_lmhead_q4_0(lp, (hipStream_t)stream));
+  return vdx_sampler_process_device(s, logits, rows, vocab, ls, uniforms, out, stream);
 }
 
 int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token) {

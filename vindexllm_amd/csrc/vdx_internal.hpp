@@ -34,6 +34,19 @@ struct CallParams {
   uint32_t *tickets;
 };
 
+// Q4_0 lm_head: logits[r*logit_stride + v] for rows r < rows, v < vocab.
+struct LmHeadParams {
+  const uint8_t *weights;  // vocab x (in_dim/32) blocks of 18 bytes, 16-byte aligned
+  const float *hidden;     // rows x in_dim (row r at hidden + r*hidden_stride)
+  int64_t hidden_stride;
+  float *logits;
+  int64_t logit_stride;
+  int32_t rows;
+  int32_t in_dim;          // multiple of 256
+  int32_t vocab;
+};
+
+hipError_t launch_lmhead_q4_0(const LmHeadParams &p, hipStream_t st);
 hipError_t launch_penalty(const CallParams &p, hipStream_t st);
 hipError_t launch_greedy(const CallParams &p, hipStream_t st);
 hipError_t launch_topk(const CallParams &p, hipStream_t st);

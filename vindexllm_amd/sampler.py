@@ -84,6 +84,11 @@ _SIGNATURES = {
     "vdx_sampler_process_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                              C.c_int64, C.c_void_p, C.POINTER(_Outputs),
                                              C.c_void_p]),
+    "vdx_lmhead_q4_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                  C.c_void_p, C.c_int64, C.c_void_p]),
+    "vdx_sampler_lmhead_q4_0_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
+                                                 C.c_int32, C.c_int32, C.c_void_p, C.c_int64,
+                                                 C.c_void_p, C.POINTER(_Outputs), C.c_void_p]),
     "vdx_sampler_add_to_history": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32]),
     "vdx_sampler_add_to_history_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32,
                                                     C.c_void_p]),
@@ -239,6 +244,42 @@ class TVdxSampler:
             C.c_void_p(st.cuda_stream)))
         return tokens
 
+    def lmhead_q4_0_device(self, weights, hidden, vocab: int, logits=None, uniforms=None,
+                           tokens=None, topk_idx=None, topk_prob=None, flags=None,
+                           uniforms_out=None, stream=None):
+        """RunUnembedding + Process (Inference.pas:327-339) on the GPU: the Q4_0
+        lm_head (``weights``: uint8 GPU tensor, vocab rows of in_dim/32 18-byte
+        blocks) over ``hidden`` (rows x in_dim float32 GPU tensor) writes logits
+        into ``logits`` (rows x >= vocab float32 GPU tensor) or the sampler's
+        workspace, and the rows are sampled as by ``process_device``."""
+        import torch
+
+        assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.is_contiguous()
+        assert weights.is_cuda and weights.dtype == torch.uint8
+        if hidden.dim() == 1:
+            hidden = hidden.view(1, -1)
+        B, D = int(hidden.shape[0]), int(hidden.shape[1])
+        if tokens is None:
+            tokens = torch.empty(B, dtype=torch.int32, device=hidden.device)
+        o = _Outputs()
+        o.tokens = tokens.data_ptr()
+        o.topk_idx = topk_idx.data_ptr() if topk_idx is not None else None
+        o.topk_prob = topk_prob.data_ptr() if topk_prob is not None else None
+        o.topk_stride = int(topk_idx.shape[-1] if topk_idx is not None else
+                            (topk_prob.shape[-1] if topk_prob is not None else 0))
+        o.flags = flags.data_ptr() if flags is not None else None
+        o.uniforms = uniforms_out.data_ptr() if uniforms_out is not None else None
+        lp, ls = None, 0
+        if logits is not None:
+            assert logits.is_cuda and logits.dtype == torch.float32
+            lp, ls = C.c_void_p(logits.data_ptr()), int(logits.stride(0))
+        st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        self._check(load_library().vdx_sampler_lmhead_q4_0_device(
+            self._h, C.c_void_p(weights.data_ptr()), C.c_void_p(hidden.data_ptr()), B, D,
+            int(vocab), lp, ls, C.c_void_p(uniforms.data_ptr()) if uniforms is not None else None,
+            C.byref(o), C.c_void_p(st.cuda_stream)))
+        return tokens
+
     # -- instrumentation ------------------------------------------------------
     def set_timing(self, enable: bool):
         self._check(load_library().vdx_sampler_set_timing(self._h, 1 if enable else 0))
@@ -284,6 +325,28 @@ class TVdxSampler:
         n = self._check(load_library().vdx_sampler_get_history(
             self._h, int(row), buf.ctypes.data_as(C.POINTER(C.c_int32)), cap, C.byref(pos)))
         return buf[:n].tolist(), pos.value
+
+
+def lmhead_q4_0(weights, hidden, vocab: int, logits=None, stream=None):
+    """The Q4_0 lm_head alone (matvec_q4_0.comp, batched): returns the rows x
+    vocab float32 logits tensor (or fills ``logits``)."""
+    import torch
+
+    assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.is_contiguous()
+    assert weights.is_cuda and weights.dtype == torch.uint8
+    if hidden.dim() == 1:
+        hidden = hidden.view(1, -1)
+    B, D = int(hidden.shape[0]), int(hidden.shape[1])
+    if logits is None:
+        logits = torch.empty(B, int(vocab), dtype=torch.float32, device=hidden.device)
+    st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+    rc = load_library().vdx_lmhead_q4_0(C.c_void_p(weights.data_ptr()),
+                                         C.c_void_p(hidden.data_ptr()), B, D, int(vocab),
+                                         C.c_void_p(logits.data_ptr()), int(logits.stride(0)),
+                                         C.c_void_p(st.cuda_stream))
+    if rc != VDX_OK:
+        raise VdxSamplerError(rc, _err(None))
+    return logits
 
 
 def version() -> str:
