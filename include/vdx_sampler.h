@@ -113,11 +113,14 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows,
  *   logits[r*logit_stride + v] = sum_e dequant(W[v][e]) * hidden[r*in_dim + e].
  * `weights`: vocab rows of in_dim/32 Q4_0 blocks (18 bytes: fp16 scale, then
  * 16 bytes of nibbles; GGUFReader.pas:264-281), 16-byte aligned; in_dim must
- * be a multiple of 256.  Every pointer is device memory.  Stream-ordered,
+ * be a multiple of 256.  `scratch` holds an element-major copy of up to 16
+ * hidden rows: at least 16*in_dim floats when rows > 1 (may be NULL when
+ * rows == 1).  Every pointer is device memory.  Stream-ordered,
  * asynchronous, allocates nothing; the message of a failure is
  * vdx_sampler_last_error(NULL). */
 int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
-                    int32_t vocab, float *logits, int64_t logit_stride, void *stream);
+                    int32_t vocab, float *logits, int64_t logit_stride, float *scratch,
+                    void *stream);
 
 /* RunUnembedding followed by Process (Inference.pas:327-339) with the logits
  * kept in HBM: the Q4_0 lm_head (as vdx_lmhead_q4_0) writes rows x vocab

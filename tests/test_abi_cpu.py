@@ -106,7 +106,9 @@ def test_lmhead_argument_errors_need_no_gpu():
         (None, hid, 1, 256, 1024, "required"),                    # weights
         (C.c_void_p(al), hid, 0, 256, 1024, "rows > 0"),          # rows
     ]
+    rc = L.vdx_lmhead_q4_0(C.c_void_p(al), hid, 2, 256, 1024, C.c_void_p(al), 1024, None, None)
+    assert rc == -1 and "scratch" in L.vdx_sampler_last_error(None).decode()
     for w, h, rows, d, v, msg in cases:
-        rc = L.vdx_lmhead_q4_0(w, h, rows, d, v, C.c_void_p(al), v, None)
+        rc = L.vdx_lmhead_q4_0(w, h, rows, d, v, C.c_void_p(al), v, C.c_void_p(al), None)
         assert rc == -1
         assert msg in L.vdx_sampler_last_error(None).decode()

@@ -38,6 +38,8 @@ struct vdx_sampler {
   // lm_head logits workspace (rows x vocab, row stride lm_stride)
   float *d_lm = nullptr;
   size_t lm_cap = 0;  // floats
+  float *d_xt = nullptr;  // element-major hidden copy (16 x in_dim)
+  int32_t xt_dim = 0;
   // host-pointer Process
   float *d_row = nullptr;
   int32_t row_cap = 0;
@@ -163,6 +165,7 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_tickets);
   (void)hipFree(s->d_row);
   (void)hipFree(s->d_lm);
+  (void)hipFree(s->d_xt);
   (void)hipFree(s->d_tok);
   for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
   if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -399,7 +402,8 @@ static const char *lmhead_check(const void *weights, const float *hidden, int32_
 }
 
 int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
-                    int32_t vocab, float *logits, int64_t logit_stride, void *stream) {
+                    int32_t vocab, float *logits, int64_t logit_stride, float *scratch,
+                    void *stream) {
   if (const char *m = lmhead_check(weights, hidden, rows, in_dim, vocab)) {
     g_call_err = m;
     return VDX_E_INVALID_ARG;
@@ -408,7 +412,12 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
     g_call_err = "lm_head: logits required, logit_stride >= vocab";
     return VDX_E_INVALID_ARG;
   }
-  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride, rows, in_dim, vocab};
+  if (rows > 1 && !scratch) {
+    g_call_err = "lm_head: scratch (16*in_dim floats) is required when rows > 1";
+    return VDX_E_INVALID_ARG;
+  }
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride,
+                  rows, in_dim, vocab, scratch};
   const hipError_t e = launch_lmhead_q4_0(lp, (hipStream_t)stream);
   if (e != hipSuccess) {
     g_call_err = std::string("lm_head launch: ") + hipGetErrorString(e);
@@ -445,7 +454,16 @@ int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const fl
   } else if (ls < vocab) {
     return fail(s, VDX_E_INVALID_ARG, "lm_head: logit_stride must be >= vocab");
   }
-  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab};
+  if (rows > 1 && in_dim > s->xt_dim) {
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+    HIP_TRY(s, hipDeviceSynchronize());
+    (void)hipFree(s->d_xt);
+    s->d_xt = nullptr;
+    s->xt_dim = 0;
+    HIP_TRY(s, hipMalloc(&s->d_xt, sizeof(float) * 16 * (size_t)in_dim));
+    s->xt_dim = in_dim;
+  }
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab, s->d_xt};
   HIP_TRY(s, launch_lmhead_q4_0(lp, (hipStream_t)stream));
   return vdx_sampler_process_device(s, logits, rows, vocab, ls, uniforms, out, stream);
 }

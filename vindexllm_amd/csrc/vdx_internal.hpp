@@ -44,6 +44,7 @@ struct LmHeadParams {
   int32_t rows;
   int32_t in_dim;          // multiple of 256
   int32_t vocab;
+  float *scratch;          // >= 16 * in_dim floats when rows > 1 (element-major hidden copy)
 };
 
 hipError_t launch_lmhead_q4_0(const LmHeadParams &p, hipStream_t st);

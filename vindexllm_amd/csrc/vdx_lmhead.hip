@@ -16,16 +16,19 @@
 // before its single rounding, as in the shader; the shader's own summation
 // order (64 strided lanes, then a tree) differs only at fp32 rounding level.
 //
-// Mapping: one thread per vocabulary row, 256 rows per workgroup.  The K
-// dimension is streamed in slices of 8 blocks (144 bytes per row): the
-// workgroup loads its 256 rows' slice with coalesced 16-byte loads, stages it
-// in LDS (176-byte row stride, so each thread's 16-byte LDS reads of its own
-// row are bank-conflict free), and prefetches the next slice while computing.
-// The hidden values are the same for every thread of the workgroup, so they
-// are read with scalar loads and enter the FMAs as SGPR operands; the weights
-// are turned into f16 (q - 8) pairs (v_perm_b32 + one packed f16 subtract per
-// two weights) that v_fma_mix_f32 consumes directly, so a weight costs
-// ~1.4 VALU ops of dequantisation plus one FMA per batch row.
+// Mapping: one thread per vocabulary row, one wave (64 rows) per workgroup.
+// The K dimension is streamed in slices of 8 blocks (144 bytes per row): the
+// wave loads its 64 rows' slice with coalesced 16-byte loads (piece P of the
+// 9 KB slice tile goes to lane P mod 64), stages it in LDS (144-byte row
+// stride: each lane's 16-byte reads of its own row are bank-conflict free)
+// and prefetches the next slice into registers while computing.  The hidden
+// values are the same for every lane, so they are read with scalar loads and
+// enter the FMAs as SGPR operands; with more than one batch row they are read
+// from a transposed copy (element-major, 16 batch rows per 64-byte line), so
+// one scalar load feeds the 16 independent accumulation chains of an element.
+// The weights are turned into f16 (q - 8) pairs (v_perm_b32 + one packed f16
+// subtract per two weights) that v_fma_mix_f32 consumes directly, so a
+// weight costs ~1.5 VALU ops of dequantisation plus one FMA per batch row.
 #include "vdx_internal.hpp"
 
 namespace vdx {
@@ -34,7 +37,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kLmPieces = 9;    // 16-byte pieces of one row per slice
-constexpr int kLmStride4 = 11;  // LDS row stride in 16-byte units (176 bytes)
 static_assert(kLmPieces * 16 == 8 * 18, "a slice is 8 Q4_0 blocks");
 
 // Two weights (q - 8) as f16 from bytes of `nib` (each 0..15): the selector
@@ -46,12 +48,11 @@ __device__ __forceinline__ f16x2 q4_pair(uint32_t nib, uint32_t sel) {
 }
 
 // One block (qs dwords q[0..3], fp16 scale bits `dbits`) for NB batch rows;
-// x points at the block's first hidden value of batch row 0, `xs` is the
-// hidden row stride, rows b >= B read row B-1 (results discarded).
+// x points at the block's first hidden value in the element-major layout
+// x[e * NB + b] (for NB == 1 the hidden row itself).
 template <int NB>
 __device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits,
-                                         const float *__restrict__ x, int64_t xs, int B,
-                                         float (&acc)[NB]) {
+                                         const float *__restrict__ x, float (&acc)[NB]) {
   f16x2 w[16];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -63,45 +64,65 @@ __device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits,
     w[9 + 2 * j] = q4_pair(hi, 0x04030402u);  // elements 16+4j+2, 16+4j+3
   }
   const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dbits & 0xFFFFu));
+  float s[NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const float *xb = x + (int64_t)(b < B ? b : B - 1) * xs;
-    float s = 0.0f;
+  for (int b = 0; b < NB; ++b) s[b] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) s = __builtin_fmaf((float)w[e >> 1][e & 1], xb[e], s);
-    acc[b] = __builtin_fmaf(d, s, acc[b]);
+  for (int e = 0; e < 32; ++e)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s[b] = __builtin_fmaf((float)w[e >> 1][e & 1], x[e * NB + b], s[b]);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = __builtin_fmaf(d, s[b], acc[b]);
+}
+
+// One slice (8 blocks = 4 block pairs of 9 dwords) of a row.
+template <int NB>
+__device__ __forceinline__ void q4_slice(const uint32_t (&r)[4 * kLmPieces], const float *__restrict__ x,
+                                         float (&acc)[NB]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t *pr = r + 9 * m;
+    // even block: scale in bytes 0-1, qs in bytes 2-17 (straddling dwords)
+    const uint32_t qa[4] = {__builtin_amdgcn_alignbyte(pr[1], pr[0], 2),
+                            __builtin_amdgcn_alignbyte(pr[2], pr[1], 2),
+                            __builtin_amdgcn_alignbyte(pr[3], pr[2], 2),
+                            __builtin_amdgcn_alignbyte(pr[4], pr[3], 2)};
+    q4_block<NB>(qa, pr[0], x + 64 * m * NB, acc);
+    // odd block: scale in bytes 18-19, qs in bytes 20-35 (dword aligned)
+    const uint32_t qb[4] = {pr[5], pr[6], pr[7], pr[8]};
+    q4_block<NB>(qb, pr[4] >> 16, x + (64 * m + 32) * NB, acc);
   }
 }
 
+// x: hidden row (NB == 1) or the element-major copy [in_dim][NB].
 template <int NB>
-__global__ __launch_bounds__(kBlock) void k_lmhead_q4_0(const uint8_t *__restrict__ wq,
-                                                        const float *__restrict__ x, int64_t xs,
-                                                        float *__restrict__ logits, int64_t ls,
-                                                        int32_t in_dim, int32_t vocab, int32_t B) {
-  __shared__ u32x4 tile[kBlock * kLmStride4];
+__global__ __launch_bounds__(64) void k_lmhead_q4_0(const uint8_t *__restrict__ wq,
+                                                    const float *__restrict__ x,
+                                                    float *__restrict__ logits, int64_t ls,
+                                                    int32_t in_dim, int32_t vocab, int32_t B) {
+  __shared__ u32x4 tile[64 * kLmPieces];
   const int t = threadIdx.x;
-  const int v0 = blockIdx.x * kBlock;
-  const int nrows = min(kBlock, vocab - v0);
+  const int v0 = blockIdx.x * 64;
+  const int nrows = min(64, vocab - v0);
   const int rowbytes = (in_dim >> 5) * 18;
   const int nslices = in_dim >> 8;
   const uint8_t *wt = wq + (int64_t)v0 * rowbytes;
 
-  // piece P = t + 256 i of a slice is piece j = P % 9 of row P / 9
-  int goff[kLmPieces], loff[kLmPieces];
+  // piece P = t + 64 i of a slice tile is piece j = P % 9 of row P / 9; rows
+  // past the vocabulary read the tile's first row (their results are not
+  // stored)
+  int goff[kLmPieces];
 #pragma unroll
   for (int i = 0; i < kLmPieces; ++i) {
-    const int P = t + kBlock * i;
+    const int P = t + 64 * i;
     const int r = P / kLmPieces, j = P - r * kLmPieces;
-    goff[i] = (r < nrows) ? r * rowbytes + 16 * j : -1;
-    loff[i] = r * kLmStride4 + j;
+    goff[i] = (r < nrows) ? r * rowbytes + 16 * j : 0;
   }
   u32x4 pre[kLmPieces];
   auto load_slice = [&](int s) {
 #pragma unroll
     for (int i = 0; i < kLmPieces; ++i)
-      pre[i] = (goff[i] >= 0)
-                   ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wt + goff[i] + 144 * s))
-                   : (u32x4){0u, 0u, 0u, 0u};
+      pre[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wt + goff[i] + 144 * s));
   };
   load_slice(0);
 
@@ -109,34 +130,21 @@ __global__ __launch_bounds__(kBlock) void k_lmhead_q4_0(const uint8_t *__restric
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
   for (int s = 0; s < nslices; ++s) {
-    if (s) __syncthreads();  // every thread has read the previous slice
+    __syncthreads();  // the previous slice has been read (one wave: no-op ordering)
 #pragma unroll
-    for (int i = 0; i < kLmPieces; ++i) tile[loff[i]] = pre[i];
+    for (int i = 0; i < kLmPieces; ++i) tile[t + 64 * i] = pre[i];
     __syncthreads();
     if (s + 1 < nslices) load_slice(s + 1);
     uint32_t r[4 * kLmPieces];
 #pragma unroll
     for (int j = 0; j < kLmPieces; ++j) {
-      const u32x4 v = tile[t * kLmStride4 + j];
+      const u32x4 v = tile[t * kLmPieces + j];
       r[4 * j] = v[0];
       r[4 * j + 1] = v[1];
       r[4 * j + 2] = v[2];
       r[4 * j + 3] = v[3];
     }
-    const float *xsl = x + 256 * s;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {  // block pair m: dwords 9m .. 9m+8
-      const uint32_t *pr = r + 9 * m;
-      // even block: scale in bytes 0-1, qs in bytes 2-17 (straddling dwords)
-      const uint32_t qa[4] = {__builtin_amdgcn_alignbyte(pr[1], pr[0], 2),
-                              __builtin_amdgcn_alignbyte(pr[2], pr[1], 2),
-                              __builtin_amdgcn_alignbyte(pr[3], pr[2], 2),
-                              __builtin_amdgcn_alignbyte(pr[4], pr[3], 2)};
-      q4_block<NB>(qa, pr[0], xsl + 64 * m, xs, B, acc);
-      // odd block: scale in bytes 18-19, qs in bytes 20-35 (dword aligned)
-      const uint32_t qb[4] = {pr[5], pr[6], pr[7], pr[8]};
-      q4_block<NB>(qb, pr[4] >> 16, xsl + 64 * m + 32, xs, B, acc);
-    }
+    q4_slice<NB>(r, x + 256 * NB * s, acc);
   }
   if (t < nrows) {
 #pragma unroll
@@ -145,22 +153,39 @@ __global__ __launch_bounds__(kBlock) void k_lmhead_q4_0(const uint8_t *__restric
   }
 }
 
+// Element-major copy of up to 16 hidden rows: xt[e * NB + b] = hidden[b][e]
+// (rows b >= B are zero).
+__global__ __launch_bounds__(256) void k_lmhead_xt(const float *__restrict__ hidden, int64_t hs,
+                                                   int32_t in_dim, int32_t B, int32_t NB,
+                                                   float *__restrict__ xt) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= in_dim * NB) return;
+  const int e = i / NB, b = i - e * NB;
+  xt[i] = (b < B) ? hidden[(int64_t)b * hs + e] : 0.0f;
+}
+
 hipError_t launch_lmhead_q4_0(const LmHeadParams &p, hipStream_t st) {
-  const dim3 grid((unsigned)((p.vocab + kBlock - 1) / kBlock));
+  const dim3 grid((unsigned)((p.vocab + 63) / 64));
   for (int b0 = 0; b0 < p.rows; b0 += 16) {
     const int B = min(16, p.rows - b0);
     const float *x = p.hidden + (int64_t)b0 * p.hidden_stride;
     float *l = p.logits + (int64_t)b0 * p.logit_stride;
-#define VDX_LM(NB)                                                                               \
-  hipLaunchKernelGGL(k_lmhead_q4_0<NB>, grid, dim3(kBlock), 0, st, p.weights, x, p.hidden_stride, \
-                     l, p.logit_stride, p.in_dim, p.vocab, B)
-    if (B == 1)
+    const int NB = (B == 1) ? 1 : (B == 2) ? 2 : (B <= 4) ? 4 : (B <= 8) ? 8 : 16;
+    if (NB > 1) {
+      hipLaunchKernelGGL(k_lmhead_xt, dim3((unsigned)((p.in_dim * NB + 255) / 256)), dim3(256), 0,
+                         st, x, p.hidden_stride, p.in_dim, B, NB, p.scratch);
+      x = p.scratch;
+    }
+#define VDX_LM(N)                                                                           \
+  hipLaunchKernelGGL(k_lmhead_q4_0<N>, grid, dim3(64), 0, st, p.weights, x, l, p.logit_stride, \
+                     p.in_dim, p.vocab, B)
+    if (NB == 1)
       VDX_LM(1);
-    else if (B == 2)
+    else if (NB == 2)
       VDX_LM(2);
-    else if (B <= 4)
+    else if (NB == 4)
       VDX_LM(4);
-    else if (B <= 8)
+    else if (NB == 8)
       VDX_LM(8);
     else
       VDX_LM(16);

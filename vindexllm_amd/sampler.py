@@ -85,7 +85,7 @@ _SIGNATURES = {
                                              C.c_int64, C.c_void_p, C.POINTER(_Outputs),
                                              C.c_void_p]),
     "vdx_lmhead_q4_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
-                                  C.c_void_p, C.c_int64, C.c_void_p]),
+                                  C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
     "vdx_sampler_lmhead_q4_0_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                                  C.c_int32, C.c_int32, C.c_void_p, C.c_int64,
                                                  C.c_void_p, C.POINTER(_Outputs), C.c_void_p]),
@@ -327,9 +327,10 @@ class TVdxSampler:
         return buf[:n].tolist(), pos.value
 
 
-def lmhead_q4_0(weights, hidden, vocab: int, logits=None, stream=None):
+def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=None):
     """The Q4_0 lm_head alone (matvec_q4_0.comp, batched): returns the rows x
-    vocab float32 logits tensor (or fills ``logits``)."""
+    vocab float32 logits tensor (or fills ``logits``).  ``scratch`` (float32
+    GPU tensor of >= 16*in_dim elements) is allocated here when not given."""
     import torch
 
     assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.is_contiguous()
@@ -339,11 +340,14 @@ def lmhead_q4_0(weights, hidden, vocab: int, logits=None, stream=None):
     B, D = int(hidden.shape[0]), int(hidden.shape[1])
     if logits is None:
         logits = torch.empty(B, int(vocab), dtype=torch.float32, device=hidden.device)
+    if scratch is None and B > 1:
+        scratch = torch.empty(16 * D, dtype=torch.float32, device=hidden.device)
     st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
     rc = load_library().vdx_lmhead_q4_0(C.c_void_p(weights.data_ptr()),
                                          C.c_void_p(hidden.data_ptr()), B, D, int(vocab),
                                          C.c_void_p(logits.data_ptr()), int(logits.stride(0)),
-                                         C.c_void_p(st.cuda_stream))
+                                         C.c_void_p(scratch.data_ptr()) if scratch is not None
+                                         else None, C.c_void_p(st.cuda_stream))
     if rc != VDX_OK:
         raise VdxSamplerError(rc, _err(None))
     return logits
