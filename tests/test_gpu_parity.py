@@ -229,6 +229,29 @@ def test_penalty_bitexact_and_repeats():
                          repeat_window=300), u, hist=hist, label=f"penalty p={p} T={T}")
 
 
+def test_fused_penalty_paths():
+    # windows of <= 256 ids with penalties > 1 are applied inside the top-K
+    # kernel (candidates penalised, logits written back by the row's last
+    # workgroup); the fast merge, the replay (TopP = 1) and small K all see
+    # the penalised row, and the logits equal the reference's in-place result
+    rng = np.random.default_rng(43)
+    for V in (20000, 262144):
+        B = 6
+        L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+        hot = rng.choice(V, 8, replace=False)
+        L[:, hot] += np.float32(7.0)
+        L[0, 5] = 0.0
+        hist = rng.integers(-5, V + 5, (B, 256)).astype(np.int32)
+        hist[:, :60] = rng.choice(hot, (B, 60))   # repeats of the largest logits
+        hist[:, 60:80] = 5
+        u = u_stream(rng, B)
+        for p in (1.1, 3.0):
+            for k, tp in ((64, 0.9), (64, 1.0), (5, 0.5)):
+                _run(L, dict(temperature=1.0, top_k=k, top_p=tp, repeat_penalty=p,
+                             repeat_window=256), u, hist=hist,
+                     label=f"fused penalty V={V} p={p} K={k} P={tp}")
+
+
 # ------------------------------------------------------ stateful sampler ----
 def _cfg(s, **kw):
     c = s.DefaultConfig()

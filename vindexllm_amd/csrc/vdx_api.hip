@@ -287,7 +287,7 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.rows = rows;
   p.vocab = vocab;
   p.nchunks = chunks_for(vocab);
-  p.vec = ((uintptr_t)logits % 16 == 0) && (row_stride % 4 == 0);
+  p.vec = ((uintptr_t)logits % 16 == 0) && (row_stride % 4 == 0) && (vocab % 4 == 0);
   p.inv_t = greedy ? 0.0f : 1.0f / c.temperature;  // Sampler.pas:325
   p.top_k = c.top_k;
   p.top_p = c.top_p;
@@ -312,9 +312,10 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.tickets = s->d_tickets;
 
   // Step 0: repetition penalty (Sampler.pas:287); the top-K kernel applies
-  // it itself for windows of up to kPenMax ids
+  // it itself for windows of up to kPenMax ids and penalties > 1 (which
+  // never raise a logit); otherwise a separate kernel runs first
   const bool pen = c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0;
-  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax) ? 1 : 0;
+  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax && c.repeat_penalty > 1.0f) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));

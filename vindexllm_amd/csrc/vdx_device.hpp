@@ -20,7 +20,7 @@ constexpr int kMergeCap = 2048;                // merge-phase LDS candidates
 constexpr int kReplayTile0 = 2048;             // first replay tile (logits)
 constexpr int kReplayTile = 4096;              // later replay tiles (logits)
 constexpr int kReplayCap = 2048;               // replay candidates per batch
-constexpr int kPenMax = 1024;                  // history ids handled inside the top-K kernel
+constexpr int kPenMax = 256;                   // history ids handled inside the top-K kernel
 
 // ---- per-row state kept in HBM -------------------------------------------------
 struct RowState {
@@ -269,24 +269,41 @@ __device__ __forceinline__ uint64_t philox4x64_10_w0(uint64_t c0, uint64_t c1,
 __device__ __forceinline__ float u24(uint64_t x) {
   return (float)(x >> 40) * (1.0f / 16777216.0f);
 }
-// One uniform for `row`: injected, or drawn (advancing that row's RNG).
-// Called by exactly one thread per row.
-__device__ __forceinline__ float draw_uniform(const KernelRng &g, int row) {
+// The state one draw for `row` needs (the injected uniform, or the row's RNG
+// state), loaded by every workgroup of the row when it starts, so the one that
+// finishes the row draws without a further round trip to memory.  The state
+// was last written by an earlier launch, never by this one.
+struct RngPre {
+  uint64_t s[4];
+  uint64_t step;
+  float u;
+};
+__device__ __forceinline__ RngPre rng_prefetch(const KernelRng &g, int row) {
+  RngPre r;  // branch-free loads: the compiler can then wait for them precisely
+  const float *up = g.uniforms ? g.uniforms + row : reinterpret_cast<const float *>(&g.rows[row].step);
+  r.u = *up;
+  r.step = g.rows[row].step;
+  r.s[0] = g.rows[row].rng[0];
+  r.s[1] = g.rows[row].rng[1];
+  r.s[2] = g.rows[row].rng[2];
+  r.s[3] = g.rows[row].rng[3];
+  return r;
+}
+// One uniform for `row` from prefetched state: injected, or drawn (advancing
+// and storing that row's RNG).  Called by exactly one thread per row.
+__device__ __forceinline__ float rng_draw(const KernelRng &g, int row, RngPre &r) {
   float u;
   if (g.uniforms) {
-    u = g.uniforms[row];
+    u = r.u;
   } else if (g.kind == 1) {
-    const uint64_t step = g.rows[row].step;
-    u = u24(philox4x64_10_w0(step, (uint64_t)row, 0, 0, g.key, 0));
-    g.rows[row].step = step + 1;
+    u = u24(philox4x64_10_w0(r.step, (uint64_t)row, 0, 0, g.key, 0));
+    g.rows[row].step = r.step + 1;
   } else {
-    uint64_t s[4] = {g.rows[row].rng[0], g.rows[row].rng[1], g.rows[row].rng[2],
-                     g.rows[row].rng[3]};
-    u = u24(xoshiro_next(s));
-    g.rows[row].rng[0] = s[0];
-    g.rows[row].rng[1] = s[1];
-    g.rows[row].rng[2] = s[2];
-    g.rows[row].rng[3] = s[3];
+    u = u24(xoshiro_next(r.s));
+    g.rows[row].rng[0] = r.s[0];
+    g.rows[row].rng[1] = r.s[1];
+    g.rows[row].rng[2] = r.s[2];
+    g.rows[row].rng[3] = r.s[3];
   }
   if (g.u_out) g.u_out[row] = u;
   return u;

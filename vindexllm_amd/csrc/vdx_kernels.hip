@@ -60,22 +60,42 @@ __device__ __forceinline__ int chunk_pos(int wv, int lane, int i) {
   return SPAN ? wv * kWaveSpan + (i >> 2) * 256 + lane * 4 + (i & 3)
               : (i >> 2) * 1024 + wv * 256 + lane * 4 + (i & 3);
 }
-// Positions at or beyond `clen` read as `fill`.
+// Positions at or beyond `clen` read as `fill`.  With VEC (16-byte aligned
+// rows whose length is a multiple of 4) every float4 group is either wholly
+// inside the row or wholly past it, so the loads are unconditional (a group
+// past the end re-reads the chunk's first group and is replaced by `fill`):
+// no branch separates them, and the compiler waits for each group on its own
+// (in-order vmcnt) instead of for all loads at once.
 template <bool VEC, bool SPAN = false>
 __device__ __forceinline__ void load_chunk(const float *__restrict__ base, int clen, int wv,
                                            int lane, float (&v)[kPerThread], float fill) {
+  if (VEC) {
 #pragma unroll
-  for (int j = 0; j < kPerThread / 4; ++j) {
-    const int local = chunk_pos<SPAN>(wv, lane, 4 * j);
-    if (VEC && local + 4 <= clen) {
-      const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base + local));
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      const int local = chunk_pos<SPAN>(wv, lane, 4 * j);
+      const f32x4 f = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4 *>(base + (local < clen ? local : 0)));
       v[4 * j + 0] = f[0];
       v[4 * j + 1] = f[1];
       v[4 * j + 2] = f[2];
       v[4 * j + 3] = f[3];
-    } else {
+    }
+    if (clen < kChunk) {  // uniform; after every load has been issued
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[4 * j + e] = (local + e < clen) ? base[local + e] : fill;
+      for (int j = 0; j < kPerThread / 4; ++j) {
+        if (chunk_pos<SPAN>(wv, lane, 4 * j) >= clen) {
+          v[4 * j + 0] = fill;
+          v[4 * j + 1] = fill;
+          v[4 * j + 2] = fill;
+          v[4 * j + 3] = fill;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int local = chunk_pos<SPAN>(wv, lane, i);
+      v[i] = (local < clen) ? base[local] : fill;
     }
   }
 }
@@ -247,6 +267,8 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
 constexpr int kMergeSpec = 8;   // candidate slots loaded per thread per round
 constexpr int kMergeTop = 512;  // keys >= T handled by the bitonic merge
 
+constexpr int kPenHash = 2 * kPenMax;  // open-addressing table of the fused penalty
+
 struct TopkSmem {
   uint32_t thr[64];
   uint32_t cnt[kWaves][64];
@@ -280,19 +302,16 @@ struct TopkSmem {
   float q_ord[kKMax];
   int32_t i_ord[kKMax];
   float v_ord[kKMax];
-  uint32_t pbits[kChunk / 32];  // fused penalty: positions of the chunk it changed
-  uint32_t pm, pen_n, pflag;
+  // fused penalty: the row's history ids, one entry per distinct id
+  int32_t hid[kPenHash];     // id, or -1
+  uint32_t hcnt[kPenHash];   // occurrences in the history
+  int32_t hfirst[kPenHash];  // first history slot holding the id
   union {
     uint64_t sk[kMergeCap];
     struct {
       float v[kReplayCap];
       int32_t i[kReplayCap];
     } rc;
-    struct {  // fused penalty (stream phase only)
-      uint64_t key[kPenMax];
-      int32_t id[kPenMax];
-      float x[kPenMax];  // the logit at id before the penalty
-    } pen;
   } buf;
 };
 
@@ -313,108 +332,115 @@ __device__ __forceinline__ int chunk_quota(int K, int S) {
   return min(K, max(8, q));
 }
 
-// Repetition penalty fused into the stream phase (Sampler.pas:285-303).  The
-// row's history (count and window) is loaded before the chunk's logits; once
-// it arrives, the logits at the history ids that fall in this chunk are
-// gathered (in flight together with the chunk).  The ids and values are listed
-// in LDS; one representative per distinct id applies the reference's sign test
-// and divide / multiply once per occurrence, stores the result in place, marks
-// the position and lists (key of the new value, index).  The stream phase then
-// skips marked positions and stores every listed value as a candidate, so the
-// register copies of the chunk are never patched.
+// Repetition penalty fused into the top-K kernel (Sampler.pas:285-303), for
+// penalties > 1 (which never raise a logit: x > 0 -> x / p < x, x < 0 ->
+// x * p < x).  Every workgroup of the row loads the row's history before its
+// chunk and, while the chunk is still in flight, counts the ids in an LDS
+// open-addressing table.  The stream phase selects candidates on the
+// unpenalised values -- a logit that is not stored is below tau_c before the
+// penalty, so also after it -- and gives every stored candidate whose index is
+// in the table its penalised value (the reference's sign test and divide /
+// multiply once per occurrence).  The row's last workgroup gathers the logits
+// at all history ids in the same round trip as the candidates and writes the
+// penalised values in place (the reference mutates its input).
 constexpr int kPenPerThread = kPenMax / kBlock;
 
 struct PenaltyPrefetch {
   int cnt;
   int32_t id[kPenPerThread];
-  float x[kPenPerThread];
 };
 
 __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
   const int W = p.hist_len;
   const int32_t *h = p.hist + (int64_t)row * W;
   pf.cnt = p.rng.rows[row].hist_count;
+  // Unconditional loads (index clamped; slots t >= count are ignored where the
+  // ids are used), and no arithmetic on them here: the chunk's loads are
+  // issued before anything waits for the ids.
 #pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) {
-    const int t = threadIdx.x + r * kBlock;
-    pf.id[r] = (t < W) ? h[t] : -1;
-  }
+  for (int r = 0; r < kPenPerThread; ++r) pf.id[r] = h[min((int)threadIdx.x + r * kBlock, W - 1)];
 }
 
-// Issued right after the chunk loads: the logits at this chunk's history ids.
-__device__ __forceinline__ void penalty_gather(const CallParams &p, int row, int c0, int clen,
-                                               PenaltyPrefetch &pf) {
-  const float *L = p.logits + (int64_t)row * p.stride;  // written in place below: not restrict
-  const int cnt = min(pf.cnt, p.hist_len);
-#pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) {
-    const int t = threadIdx.x + r * kBlock;
-    const int id = pf.id[r];
-    pf.x[r] = (t < cnt && id >= c0 && id < c0 + clen) ? L[id] : 0.0f;
-  }
+__device__ __forceinline__ uint32_t pen_hash(int32_t id) {
+  return ((uint32_t)id * 2654435761u) >> (32 - 9);  // kPenHash = 512 slots
 }
+static_assert(kPenHash == 512, "pen_hash yields 9 bits");
 
-// Leaves sm.pen_n listed (key of the new value, index) pairs in sm.pen_key.
-__device__ __forceinline__ void fused_penalty(const CallParams &p, int row, int c0, int clen,
-                                              const PenaltyPrefetch &pf, TopkSmem &sm) {
+// Builds the table from the prefetched ids (two barriers; the chunk's loads
+// stay in flight).
+__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, TopkSmem &sm) {
   const int tid = threadIdx.x;
-  float *L = p.logits + (int64_t)row * p.stride;
-  const int cnt = min(pf.cnt, p.hist_len);
-  for (int w = tid; w < kChunk / 32; w += kBlock) sm.pbits[w] = 0u;
-  if (tid == 0) {
-    sm.pm = 0u;
-    sm.pen_n = 0u;
-    sm.pflag = 0u;
+  for (int i = tid; i < kPenHash; i += kBlock) {
+    sm.hid[i] = -1;
+    sm.hcnt[i] = 0u;
+    sm.hfirst[i] = 0x7FFFFFFF;
   }
   __syncthreads();
+  const int cnt = min(pf.cnt, p.hist_len);
 #pragma unroll
   for (int r = 0; r < kPenPerThread; ++r) {
     const int t = tid + r * kBlock;
     const int id = pf.id[r];
-    if (t < cnt && id >= c0 && id < c0 + clen) {
-      const uint32_t q = atomicAdd(&sm.pm, 1u);
-      sm.buf.pen.id[q] = id;  // q < cnt <= window <= kPenMax
-      sm.buf.pen.x[q] = pf.x[r];
-    }
-  }
-  __syncthreads();
-  const int m = (int)sm.pm;
-  for (int e = tid; e < m; e += kBlock) {
-    const int id = sm.buf.pen.id[e];
-    int k = 0;
-    bool rep = true;
-    for (int f = 0; f < m; ++f) {
-      if (sm.buf.pen.id[f] == id) {
-        rep = rep && (f >= e);
-        ++k;
+    if (t < cnt && id >= 0 && id < p.vocab) {
+      uint32_t h = pen_hash(id);
+      for (;;) {  // at most cnt <= kPenHash / 2 distinct ids: a free slot exists
+        const int old = atomicCAS(&sm.hid[h], -1, id);
+        if (old == -1 || old == id) break;
+        h = (h + 1u) & (uint32_t)(kPenHash - 1);
       }
-    }
-    if (rep) {
-      const float x = penalise(sm.buf.pen.x[e], k, p.penalty);
-      xstoref(&L[id], x);
-      if (!(x <= 3.4028235e38f)) sm.pflag = 1u;  // NaN, or +inf (e.g. a boost that overflowed)
-      atomicOr(&sm.pbits[(id - c0) >> 5], 1u << ((id - c0) & 31));
-      const uint32_t q = atomicAdd(&sm.pen_n, 1u);
-      sm.buf.pen.key[q] = ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)id);
+      atomicAdd(&sm.hcnt[h], 1u);
+      atomicMin(&sm.hfirst[h], t);
     }
   }
   __syncthreads();
+}
+
+// Slot of `id` in the table, or -1.
+__device__ __forceinline__ int pen_find(const TopkSmem &sm, int32_t id) {
+  uint32_t h = pen_hash(id);
+  for (int n = 0; n < kPenHash; ++n) {
+    const int32_t e = sm.hid[h];
+    if (e == id) return (int)h;
+    if (e == -1) return -1;
+    h = (h + 1u) & (uint32_t)(kPenHash - 1);
+  }
+  return -1;
+}
+
+// The value the reference's penalty leaves at index `id` (x before it).
+__device__ __forceinline__ float pen_value(const CallParams &p, const TopkSmem &sm, int32_t id, float x) {
+  const int h = pen_find(sm, id);
+  return (h < 0) ? x : penalise(x, (int)sm.hcnt[h], p.penalty);
+}
+
+// Last workgroup of the row: the logits at the history ids (gathered before
+// the merge) are penalised once per distinct id and stored in place.
+__device__ __forceinline__ void penalty_write_back(const CallParams &p, int row, const PenaltyPrefetch &pf,
+                                                   const float (&gx)[kPenPerThread], const TopkSmem &sm) {
+  float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
+  const int cnt = min(pf.cnt, p.hist_len);
+#pragma unroll
+  for (int r = 0; r < kPenPerThread; ++r) {
+    const int t = threadIdx.x + r * kBlock;
+    const int id = pf.id[r];
+    if (t < cnt && id >= 0 && id < p.vocab) {
+      const int h = pen_find(sm, id);
+      if (h >= 0 && sm.hfirst[h] == t) xstoref(&Lw[id], penalise(gx[r], (int)sm.hcnt[h], p.penalty));
+    }
+  }
 }
 
 template <bool VEC>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
-                                            ChunkMeta *__restrict__ meta, TopkSmem &sm) {
+                                            ChunkMeta *__restrict__ meta, const PenaltyPrefetch &pf,
+                                            TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
-  PenaltyPrefetch pf;
   const bool pen = p.fuse_penalty != 0;
-  if (pen) penalty_prefetch(p, row, pf);
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
-  if (pen) penalty_gather(p, row, c0, clen, pf);
-  if (pen) fused_penalty(p, row, c0, clen, pf, sm);
-  const uint32_t npen = pen ? sm.pen_n : 0u;
+  if (pen) penalty_table(p, pf, sm);
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
@@ -472,45 +498,27 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   // (wave_cap), at a running wave count plus the lane's rank in the ballot,
   // so no block-wide count or barrier is needed.  Full chunks test one float4
   // group maximum per compare and branch (wave-uniform) only into groups in
-  // which some lane passes.  Positions changed by the fused penalty are
-  // skipped; their new values are stored from the penalty's list.
+  // which some lane passes.
   const bool all = (tau == 0u);
   const int cap = wave_cap(clen);
   Cand *wreg = cand + wv * cap;
   uint32_t wc = 0u;  // wave-uniform
-  if (npen) {
-    for (uint32_t i0 = 0u; i0 < npen; i0 += 64u) {
-      const uint32_t i = i0 + (uint32_t)lane;
-      uint64_t k = 0ull;
-      bool own = false;
-      if (i < npen) {
-        k = sm.buf.pen.key[i];
-        own = (((((int)(~(uint32_t)k)) - c0) >> 8) & 3) == wv && (all || (uint32_t)(k >> 32) >= tau);
-      }
-      const uint64_t ob = __ballot(own);
-      if (ob) {
-        const uint32_t q = wc + lane_rank(ob);
-        if (own && q < (uint32_t)cap) xstore(&wreg[q], k);
-        wc += (uint32_t)__popcll(ob);
-      }
-    }
-  }
   if (clen == kChunk && !all) {
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
       if (__ballot(gmax4(v, j) >= tf)) {
         const int l0 = chunk_pos(wv, lane, 4 * j);
-        uint32_t pb = 0u;
-        if (npen) pb = (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool hit = v[4 * j + e] >= tf && !((pb >> e) & 1u);
+          const bool hit = v[4 * j + e] >= tf;
           const uint64_t hb = __ballot(hit);
           if (hb) {
             const uint32_t q = wc + lane_rank(hb);
-            if (hit && q < (uint32_t)cap)
-              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
-                                   (uint32_t)(~(uint32_t)(c0 + l0 + e)));
+            if (hit && q < (uint32_t)cap) {
+              const int idx = c0 + l0 + e;
+              const float x = pen ? pen_value(p, sm, idx, v[4 * j + e]) : v[4 * j + e];
+              xstore(&wreg[q], ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)idx));
+            }
             wc += (uint32_t)__popcll(hb);
           }
         }
@@ -522,17 +530,17 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
       const int l0 = chunk_pos(wv, lane, 4 * j);
       const bool gp = (l0 < clen) && (all || gmax4(v, j) >= tf);
       if (__ballot(gp)) {
-        uint32_t pb = 0u;
-        if (npen) pb = gp ? (sm.pbits[l0 >> 5] >> (l0 & 31)) & 0xFu : 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool hit = gp && (l0 + e < clen) && !((pb >> e) & 1u) && (all || v[4 * j + e] >= tf);
+          const bool hit = gp && (l0 + e < clen) && (all || v[4 * j + e] >= tf);
           const uint64_t hb = __ballot(hit);
           if (hb) {
             const uint32_t q = wc + lane_rank(hb);
-            if (hit && q < (uint32_t)cap)
-              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) |
-                                   (uint32_t)(~(uint32_t)(c0 + l0 + e)));
+            if (hit && q < (uint32_t)cap) {
+              const int idx = c0 + l0 + e;
+              const float x = pen ? pen_value(p, sm, idx, v[4 * j + e]) : v[4 * j + e];
+              xstore(&wreg[q], ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)idx));
+            }
             wc += (uint32_t)__popcll(hb);
           }
         }
@@ -541,8 +549,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   }
   if (lane == 0) xstore32(&meta->n[wv], wc);
   if (tid == 0) {
-    uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
-    if (pen) fl |= sm.pflag;
+    const uint32_t fl = sm.wflag[0] | sm.wflag[1] | sm.wflag[2] | sm.wflag[3];
     xstore(&meta->w, (uint64_t)tau | ((uint64_t)fl << 32));
   }
 }
@@ -614,16 +621,33 @@ __device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, TopkSmem &sm, u
   return prefix;
 }
 
-// ---- in-wave bitonic network: 64 keys, one per lane, sorted descending --------------
-// Lane exchanges: DPP quad_perm (xor 1, 2), DPP row_ror:8 (xor 8), ds_swizzle in
-// bit mode (xor 4, 16 inside 32-lane halves) and ds_bpermute (xor 32).
+// ---- in-wave bitonic network: 64 keys, one per lane ------------------------------------
+// Every lane exchange stays on the VALU: DPP quad_perm (xor 1, 2), DPP row
+// shifts by 4 in both directions (xor 4), DPP row_ror:8 (xor 8), and gfx950's
+// v_permlane16_swap / v_permlane32_swap (xor 16, 32), so a compare-exchange
+// step never waits on the LDS crossbar.
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane32(uint32_t v) {
-  if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
-  else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
-  else if constexpr (J == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
-  else if constexpr (J == 4 || J == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (J << 10));
-  else return (uint32_t)__builtin_amdgcn_ds_bpermute((lane_id() ^ J) << 2, (int)v);
+  const int l = lane_id();
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (J == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);  // lane + 4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);  // lane - 4
+    return (l & 4) ? dn : up;
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+  } else if constexpr (J == 16) {
+    // swap(v, v): first = rows {0,0,2,2}, second = rows {1,1,3,3}
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (l & 16) ? r[0] : r[1];
+  } else {
+    // swap(v, v): first = halves {lo,lo}, second = halves {hi,hi}
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (l & 32) ? r[0] : r[1];
+  }
 }
 template <int J>
 __device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
@@ -635,37 +659,41 @@ __device__ __forceinline__ uint64_t reverse_lanes64(uint64_t v) {
          (uint32_t)__builtin_amdgcn_ds_bpermute(a, (int)(uint32_t)v);
 }
 // One compare-exchange step of the network: blocks of size K sorted in
-// alternating directions (descending where lane & K == 0; all descending at
-// K = 64), partners J lanes apart.
-template <int K, int J>
+// alternating directions (all in the final direction at K = 64), partners J
+// lanes apart; ASC = ascending final order (lower lane keeps the smaller key).
+template <int K, int J, bool ASC = false>
 __device__ __forceinline__ uint64_t bitonic_step(uint64_t x) {
   const uint64_t y = xor_lane64<J>(x);
   const int l = lane_id();
-  const bool keep_max = ((l & J) == 0) == ((K >= 64) || ((l & K) == 0));
+  const bool keep_max = (((l & J) == 0) == ((K >= 64) || ((l & K) == 0))) != ASC;
   return (keep_max == (x > y)) ? x : y;
 }
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t x) {
-  x = bitonic_step<2, 1>(x);
-  x = bitonic_step<4, 2>(x);  x = bitonic_step<4, 1>(x);
-  x = bitonic_step<8, 4>(x);  x = bitonic_step<8, 2>(x);  x = bitonic_step<8, 1>(x);
-  x = bitonic_step<16, 8>(x); x = bitonic_step<16, 4>(x); x = bitonic_step<16, 2>(x);
-  x = bitonic_step<16, 1>(x);
-  x = bitonic_step<32, 16>(x); x = bitonic_step<32, 8>(x); x = bitonic_step<32, 4>(x);
-  x = bitonic_step<32, 2>(x);  x = bitonic_step<32, 1>(x);
-  x = bitonic_step<64, 32>(x); x = bitonic_step<64, 16>(x); x = bitonic_step<64, 8>(x);
-  x = bitonic_step<64, 4>(x);  x = bitonic_step<64, 2>(x);  x = bitonic_step<64, 1>(x);
+template <bool ASC = false>
+__device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
+  x = bitonic_step<2, 1, ASC>(x);
+  x = bitonic_step<4, 2, ASC>(x);  x = bitonic_step<4, 1, ASC>(x);
+  x = bitonic_step<8, 4, ASC>(x);  x = bitonic_step<8, 2, ASC>(x);  x = bitonic_step<8, 1, ASC>(x);
+  x = bitonic_step<16, 8, ASC>(x); x = bitonic_step<16, 4, ASC>(x); x = bitonic_step<16, 2, ASC>(x);
+  x = bitonic_step<16, 1, ASC>(x);
+  x = bitonic_step<32, 16, ASC>(x); x = bitonic_step<32, 8, ASC>(x); x = bitonic_step<32, 4, ASC>(x);
+  x = bitonic_step<32, 2, ASC>(x);  x = bitonic_step<32, 1, ASC>(x);
+  x = bitonic_step<64, 32, ASC>(x); x = bitonic_step<64, 16, ASC>(x); x = bitonic_step<64, 8, ASC>(x);
+  x = bitonic_step<64, 4, ASC>(x);  x = bitonic_step<64, 2, ASC>(x);  x = bitonic_step<64, 1, ASC>(x);
   return x;
 }
-// A bitonic sequence of 64 keys to descending order.
-__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t x) {
-  x = bitonic_step<64, 32>(x); x = bitonic_step<64, 16>(x); x = bitonic_step<64, 8>(x);
-  x = bitonic_step<64, 4>(x);  x = bitonic_step<64, 2>(x);  x = bitonic_step<64, 1>(x);
+// A bitonic sequence of 64 keys to sorted order.
+template <bool ASC = false>
+__device__ __forceinline__ uint64_t wave_merge(uint64_t x) {
+  x = bitonic_step<64, 32, ASC>(x); x = bitonic_step<64, 16, ASC>(x); x = bitonic_step<64, 8, ASC>(x);
+  x = bitonic_step<64, 4, ASC>(x);  x = bitonic_step<64, 2, ASC>(x);  x = bitonic_step<64, 1, ASC>(x);
   return x;
 }
-// Top 64 of two descending 64-key lists held by one wave: the lane-wise
-// maximum of a and reversed b is bitonic and holds the 64 largest.
-__device__ __forceinline__ uint64_t wave_top64(uint64_t a, uint64_t b_reversed) {
-  return wave_merge_desc(a > b_reversed ? a : b_reversed);
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t x) { return wave_sort<false>(x); }
+// Top 64 of two sorted 64-key lists held by one wave, one descending and one
+// ascending: their lane-wise maximum is bitonic and holds the 64 largest.
+template <bool ASC = false>
+__device__ __forceinline__ uint64_t wave_top64(uint64_t a, uint64_t b_opposite) {
+  return wave_merge<ASC>(a > b_opposite ? a : b_opposite);
 }
 
 // Candidate slot i of the row (chunk i / kCandCap) holds a stored key.  Only
@@ -832,6 +860,117 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
   return true;
 }
 
+
+// Fast merge for rows of at most kFastChunks chunks, with no block-wide
+// compaction: every wave reads the chunk records itself (T = max tau_c) and
+// filters the candidate slots of chunks wv, wv+4, ... (loaded in the same round
+// trip as the records) against T into its own LDS list, sorts it in registers
+// (descending in waves 0 and 2, ascending in 1 and 3), and the four sorted
+// lists merge pairwise by lane-wise maxima and bitonic merges.  Returns 1 when
+// sm.topkey holds the row's top K, 0 when the row must be replayed (NaN/+inf,
+// or the K-th value tied with a stored key outside the set), -1 when the
+// general merge must run (a region overflowed, fewer than K keys reach T, or a
+// wave list would exceed kWaveCand).
+constexpr int kFastChunks = 16;
+constexpr int kWaveCand = 256;
+static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + kWaves * 64 <= kMergeCap,
+              "fast merge buffers");
+
+__device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const ChunkMeta *__restrict__ cm,
+                                                const Cand *__restrict__ cand_row, TopkSmem &sm) {
+  const int lane = lane_id(), wv = threadIdx.x >> 6;
+  // one round trip: the records (lane c < S) and this wave's candidate slots
+  const int lc = min(lane, S - 1);
+  const uint64_t w0 = xload(&cm[lc].w);
+  const uint64_t n01 = xload(reinterpret_cast<const uint64_t *>(&cm[lc].n[0]));
+  const uint64_t n23 = xload(reinterpret_cast<const uint64_t *>(&cm[lc].n[2]));
+  uint64_t kk[2 * (kFastChunks / kWaves)];
+#pragma unroll
+  for (int j = 0; j < kFastChunks / kWaves; ++j) {  // unconditional (clamped): precise waits
+    const int c = min(wv + kWaves * j, S - 1);
+    kk[2 * j] = xload(&cand_row[c * kCandCap + 2 * lane]);
+    kk[2 * j + 1] = xload(&cand_row[c * kCandCap + 2 * lane + 1]);
+  }
+  const uint32_t cap = (lane < S) ? (uint32_t)wave_cap(min(kChunk, V - lane * kChunk)) : 0u;
+  const uint32_t n0 = (uint32_t)n01, n1 = (uint32_t)(n01 >> 32), n2 = (uint32_t)n23,
+                 n3 = (uint32_t)(n23 >> 32);
+  const bool ovf = n0 > cap || n1 > cap || n2 > cap || n3 > cap;
+  const uint32_t counts = min(n0, cap) | (min(n1, cap) << 8) | (min(n2, cap) << 16) | (min(n3, cap) << 24);
+  const uint32_t tau = (lane < S) ? (ovf ? 0xFFFFFFFFu : (uint32_t)w0) : 0u;
+  const uint32_t T = wave_max_u32(tau);
+  const uint32_t fl = wave_or_u32((lane < S) ? (uint32_t)(w0 >> 32) : 0u);
+  if (fl) return 0;                  // the same in every wave
+  if (T == 0xFFFFFFFFu) return -1;
+
+  // keys >= T of this wave's chunks, compacted by ballot into its LDS list
+  const uint64_t thr = (uint64_t)T << 32;
+  uint64_t *wl = sm.buf.sk + wv * kWaveCand;
+  uint32_t nw = 0u;
+#pragma unroll
+  for (int j = 0; j < kFastChunks / kWaves; ++j) {
+    const int c = wv + kWaves * j;
+    if (c >= S) break;  // uniform
+    const uint32_t cnt = readlane32(counts, c);
+    const uint32_t ccap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk));
+    const int sh = ccap == 128u ? 7 : (ccap == 64u ? 6 : 5);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t slot = 2u * (uint32_t)lane + (uint32_t)e;
+      const uint32_t have = (cnt >> (8 * (slot >> sh))) & 0xFFu;
+      const bool ok = (slot & (ccap - 1u)) < have && kk[2 * j + e] >= thr;
+      const uint64_t b = __ballot(ok);
+      const uint32_t q = nw + lane_rank(b);
+      if (ok && q < (uint32_t)kWaveCand) wl[q] = kk[2 * j + e];
+      nw += (uint32_t)__popcll(b);
+    }
+  }
+  // this wave's top 64, sorted (ascending in odd waves)
+  const bool asc = (wv & 1) != 0;
+  uint64_t x = ((uint32_t)lane < nw) ? wl[lane] : 0ull;
+  x = asc ? wave_sort<true>(x) : wave_sort<false>(x);
+  for (uint32_t base = 64u; base < min(nw, (uint32_t)kWaveCand); base += 64u) {
+    uint64_t y = (base + (uint32_t)lane < nw) ? wl[base + lane] : 0ull;
+    y = asc ? wave_sort<false>(y) : wave_sort<true>(y);
+    x = asc ? wave_top64<true>(x, y) : wave_top64<false>(x, y);
+  }
+  uint64_t *R = sm.buf.sk + kWaves * kWaveCand;  // four sorted lists of 64
+  R[wv * 64 + lane] = x;
+  if (lane == 0) sm.cnt[0][wv] = nw;
+  __syncthreads();
+  uint32_t nf = 0u;
+  bool big = false;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    nf += sm.cnt[0][w];
+    big = big || sm.cnt[0][w] > (uint32_t)kWaveCand;
+  }
+  if (big || nf < (uint32_t)K) return -1;  // the same in every wave
+  if (wv == 0 || wv == 2) {
+    x = (wv == 2) ? wave_top64<true>(x, R[(wv + 1) * 64 + lane]) : wave_top64<false>(x, R[(wv + 1) * 64 + lane]);
+    R[wv * 64 + lane] = x;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    x = wave_top64<false>(x, R[2 * 64 + lane]);
+    // The reference keeps the top K; if the K-th value is shared by a stored
+    // key outside them, which tied logits it keeps depends on its slot order.
+    const uint32_t vk = (uint32_t)(readlane64(x, K - 1) >> 32);
+    const uint32_t inset = (uint32_t)__popcll(__ballot(lane < K && (uint32_t)(x >> 32) == vk));
+    uint32_t tied = 0u;
+    for (int w = 0; w < kWaves; ++w) {
+      const uint32_t nw2 = sm.cnt[0][w];
+      for (uint32_t j0 = 0u; j0 < nw2; j0 += 64u) {
+        const uint32_t j = j0 + (uint32_t)lane;
+        tied += (uint32_t)__popcll(
+            __ballot(j < nw2 && (uint32_t)(sm.buf.sk[w * kWaveCand + j] >> 32) == vk));
+      }
+    }
+    if (lane < K) sm.topkey[lane] = x;
+    if (lane == 0) sm.ntop = (tied > inset) ? -1 : K;
+  }
+  __syncthreads();
+  return sm.ntop == K ? 1 : 0;
+}
 
 // Merge (the last workgroup of the row).  One round trip loads the chunk
 // records and, speculatively, the first kMergeSpec * kBlock candidate slots.
@@ -1351,16 +1490,44 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
+  RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
+  PenaltyPrefetch pf;
+  if (p.fuse_penalty) penalty_prefetch(p, row, pf);  // issued before the chunk
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
-                        cm + chunk, sm);
+                        cm + chunk, pf, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
+  float gx[kPenPerThread];
+  if (p.fuse_penalty) {  // the logits at the history ids, gathered with the candidates
+    const int cnt = min(pf.cnt, p.hist_len);
+#pragma unroll
+    for (int r = 0; r < kPenPerThread; ++r) {
+      const int t = threadIdx.x + r * kBlock;
+      const int id = pf.id[r];
+      gx[r] = (t < cnt && id >= 0 && id < p.vocab) ? xloadf(&L[id]) : 0.0f;
+    }
+  }
   if (threadIdx.x == 0) {
-    sm.uval = draw_uniform(p.rng, row);
+    sm.uval = rng_draw(p.rng, row, rp);
     sm.replay = 1;
   }
   __syncthreads();
-  if (topk_merge<VEC>(L, p.vocab, S, K, cm, cr, sm)) topk_fast(p, row, sm);
-  if (sm.replay) topk_replay(p, row, sm);
+  int mr = (S <= kFastChunks) ? topk_merge_waves(p.vocab, S, K, cm, cr, sm) : -1;
+  if (p.fuse_penalty) {
+    penalty_write_back(p, row, pf, gx, sm);
+    if (mr <= 0) {  // the paths below re-read the row: the stores must be visible
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  if (mr < 0) mr = topk_merge<VEC>(L, p.vocab, S, K, cm, cr, sm) ? 1 : 0;
+  if (mr > 0) topk_fast(p, row, sm);
+  if (sm.replay) {
+    if (p.fuse_penalty) {  // the replay re-reads the row: the stores must be visible
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    topk_replay(p, row, sm);
+  }
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
@@ -1448,6 +1615,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   FullMeta *fm = p.fmeta + (int64_t)row * S;
   const int c0 = chunk * kChunk;
   const int clen = min(kChunk, V - c0);
+  RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
   float v[kPerThread];
   load_chunk<VEC, true>(L + c0, clen, wv, lane, v, -INFINITY);
 
@@ -1517,7 +1685,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
   if (!last_of_row(p.tickets, row, S, &sm.last)) return;
 
   // ---- finish (last workgroup of the row) ----
-  if (tid == 0) sm.u = draw_uniform(p.rng, row);
+  if (tid == 0) sm.u = rng_draw(p.rng, row, rp);
   float mc = -INFINITY;
   uint32_t fl = 0u;
   double dc = 0.0;
