@@ -283,6 +283,7 @@ struct TopkSmem {
   uint32_t rbin, rneed, rcnt;
   uint32_t ngt;
   int32_t ntop;
+  int32_t mres;
   uint64_t topsel[kKMax];
   uint64_t topkey[kKMax];
   float uval;
@@ -696,6 +697,30 @@ __device__ __forceinline__ uint64_t wave_top64(uint64_t a, uint64_t b_opposite) 
   return wave_merge<ASC>(a > b_opposite ? a : b_opposite);
 }
 
+// Two independent sorts interleaved step by step (x descending, y
+// ascending): the second network's instructions fill the first one's
+// latency, so both take about the time of one.
+template <int K, int J>
+__device__ __forceinline__ void bitonic_step2(uint64_t &x, uint64_t &y) {
+  const uint64_t xo = xor_lane64<J>(x);
+  const uint64_t yo = xor_lane64<J>(y);
+  const int l = lane_id();
+  const bool keep_max = ((l & J) == 0) == ((K >= 64) || ((l & K) == 0));
+  x = (keep_max == (x > xo)) ? x : xo;
+  y = (keep_max != (y > yo)) ? y : yo;
+}
+__device__ __forceinline__ void wave_sort2(uint64_t &x, uint64_t &y) {
+  bitonic_step2<2, 1>(x, y);
+  bitonic_step2<4, 2>(x, y);  bitonic_step2<4, 1>(x, y);
+  bitonic_step2<8, 4>(x, y);  bitonic_step2<8, 2>(x, y);  bitonic_step2<8, 1>(x, y);
+  bitonic_step2<16, 8>(x, y); bitonic_step2<16, 4>(x, y); bitonic_step2<16, 2>(x, y);
+  bitonic_step2<16, 1>(x, y);
+  bitonic_step2<32, 16>(x, y); bitonic_step2<32, 8>(x, y); bitonic_step2<32, 4>(x, y);
+  bitonic_step2<32, 2>(x, y);  bitonic_step2<32, 1>(x, y);
+  bitonic_step2<64, 32>(x, y); bitonic_step2<64, 16>(x, y); bitonic_step2<64, 8>(x, y);
+  bitonic_step2<64, 4>(x, y);  bitonic_step2<64, 2>(x, y);  bitonic_step2<64, 1>(x, y);
+}
+
 // Candidate slot i of the row (chunk i / kCandCap) holds a stored key.  Only
 // the row's last chunk can be short, so every other chunk has regions of
 // kCandCap / kWaves slots; `last_sh` is log2 of the last chunk's region size.
@@ -873,7 +898,7 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
 // wave list would exceed kWaveCand).
 constexpr int kFastChunks = 16;
 constexpr int kWaveCand = 256;
-static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + kWaves * 64 <= kMergeCap,
+static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMergeCap && kBlock == 256,
               "fast merge buffers");
 
 __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const ChunkMeta *__restrict__ cm,
@@ -905,7 +930,7 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
   // keys >= T of this wave's chunks, compacted by ballot into its LDS list
   const uint64_t thr = (uint64_t)T << 32;
   uint64_t *wl = sm.buf.sk + wv * kWaveCand;
-  uint32_t nw = 0u;
+  uint32_t nw = 0u, vmax_k = 0u;
 #pragma unroll
   for (int j = 0; j < kFastChunks / kWaves; ++j) {
     const int c = wv + kWaves * j;
@@ -921,56 +946,93 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
       const uint64_t b = __ballot(ok);
       const uint32_t q = nw + lane_rank(b);
       if (ok && q < (uint32_t)kWaveCand) wl[q] = kk[2 * j + e];
+      if (ok) vmax_k = max(vmax_k, (uint32_t)(kk[2 * j + e] >> 32));
       nw += (uint32_t)__popcll(b);
     }
   }
-  // this wave's top 64, sorted (ascending in odd waves)
-  const bool asc = (wv & 1) != 0;
-  uint64_t x = ((uint32_t)lane < nw) ? wl[lane] : 0ull;
-  x = asc ? wave_sort<true>(x) : wave_sort<false>(x);
-  for (uint32_t base = 64u; base < min(nw, (uint32_t)kWaveCand); base += 64u) {
-    uint64_t y = (base + (uint32_t)lane < nw) ? wl[base + lane] : 0ull;
-    y = asc ? wave_sort<false>(y) : wave_sort<true>(y);
-    x = asc ? wave_top64<true>(x, y) : wave_top64<false>(x, y);
+  // Wave 0 alone from here: one radix digit (the highest bits in which T and
+  // the largest key differ; the bits above are common to every key >= T)
+  // narrows the nf keys to the m that can be in the top K: every key in bins
+  // above the bin holding the K-th key, and that bin.  With m <= 128 they are
+  // sorted as two interleaved 64-key networks and one merge.
+  vmax_k = wave_max_u32(vmax_k);
+  if (lane == 0) {
+    sm.cnt[0][wv] = nw;
+    sm.cnt[1][wv] = vmax_k;
   }
-  uint64_t *R = sm.buf.sk + kWaves * kWaveCand;  // four sorted lists of 64
-  R[wv * 64 + lane] = x;
-  if (lane == 0) sm.cnt[0][wv] = nw;
+  sm.hist[threadIdx.x] = 0u;  // kBlock == 256 bins
   __syncthreads();
-  uint32_t nf = 0u;
+  if (wv != 0) return 2;  // waves 1..3 wait at the final barrier of the caller
+  uint32_t nf = 0u, kmax = 0u;
   bool big = false;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     nf += sm.cnt[0][w];
+    kmax = max(kmax, sm.cnt[1][w]);
     big = big || sm.cnt[0][w] > (uint32_t)kWaveCand;
   }
-  if (big || nf < (uint32_t)K) return -1;  // the same in every wave
-  if (wv == 0 || wv == 2) {
-    x = (wv == 2) ? wave_top64<true>(x, R[(wv + 1) * 64 + lane]) : wave_top64<false>(x, R[(wv + 1) * 64 + lane]);
-    R[wv * 64 + lane] = x;
+  if (big || nf < (uint32_t)K || kmax == T) return -1;
+  const int shift = (31 - __clz((int)(T ^ kmax))) & ~7;
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t nw2 = sm.cnt[0][w];
+    for (uint32_t i = (uint32_t)lane; i < nw2; i += 64u)
+      atomicAdd(&sm.hist[(uint32_t)(sm.buf.sk[w * kWaveCand + i] >> (32 + shift)) & 255u], 1u);
   }
-  __syncthreads();
-  if (wv == 0) {
-    x = wave_top64<false>(x, R[2 * 64 + lane]);
-    // The reference keeps the top K; if the K-th value is shared by a stored
-    // key outside them, which tied logits it keeps depends on its slot order.
-    const uint32_t vk = (uint32_t)(readlane64(x, K - 1) >> 32);
-    const uint32_t inset = (uint32_t)__popcll(__ballot(lane < K && (uint32_t)(x >> 32) == vk));
-    uint32_t tied = 0u;
-    for (int w = 0; w < kWaves; ++w) {
-      const uint32_t nw2 = sm.cnt[0][w];
-      for (uint32_t j0 = 0u; j0 < nw2; j0 += 64u) {
-        const uint32_t j = j0 + (uint32_t)lane;
-        tied += (uint32_t)__popcll(
-            __ballot(j < nw2 && (uint32_t)(sm.buf.sk[w * kWaveCand + j] >> 32) == vk));
-      }
+  // bins from the top: lane l holds bins 255-4l .. 252-4l
+  const int b0 = 255 - 4 * lane;
+  const uint32_t h0 = sm.hist[b0], h1 = sm.hist[b0 - 1], h2 = sm.hist[b0 - 2], h3 = sm.hist[b0 - 3];
+  const uint32_t incl = wave_incl_scan_u32(h0 + h1 + h2 + h3);
+  const uint32_t excl = incl - (h0 + h1 + h2 + h3);
+  // first lane whose running count reaches K, then the bin inside it
+  const uint64_t reach = __ballot(incl >= (uint32_t)K);
+  const int ls = __ffsll((unsigned long long)reach) - 1;  // reach != 0: nf >= K
+  uint32_t bstar = 0u, m = 0u;
+  {
+    const uint32_t e0 = readlane32(excl, ls);
+    const uint32_t g0 = readlane32(h0, ls), g1 = readlane32(h1, ls), g2 = readlane32(h2, ls),
+                   g3 = readlane32(h3, ls);
+    const uint32_t bb = 255u - 4u * (uint32_t)ls;
+    if (e0 + g0 >= (uint32_t)K) { bstar = bb; m = e0 + g0; }
+    else if (e0 + g0 + g1 >= (uint32_t)K) { bstar = bb - 1u; m = e0 + g0 + g1; }
+    else if (e0 + g0 + g1 + g2 >= (uint32_t)K) { bstar = bb - 2u; m = e0 + g0 + g1 + g2; }
+    else { bstar = bb - 3u; m = e0 + g0 + g1 + g2 + g3; }
+  }
+  if (m > 128u) return -1;
+  // the m keys with digit >= bstar, and the largest value key below them
+  uint64_t *sel = sm.buf.sk + kWaves * kWaveCand;
+  uint32_t ns = 0u, below = 0u;
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t nw2 = sm.cnt[0][w];
+    for (uint32_t i0 = 0u; i0 < nw2; i0 += 64u) {
+      const uint32_t i = i0 + (uint32_t)lane;
+      const uint64_t k = (i < nw2) ? sm.buf.sk[w * kWaveCand + i] : 0ull;
+      const bool in = i < nw2 && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
+      const uint64_t bm = __ballot(in);
+      if (in) sel[ns + lane_rank(bm)] = k;
+      else if (i < nw2) below = max(below, (uint32_t)(k >> 32));
+      ns += (uint32_t)__popcll(bm);
     }
-    if (lane < K) sm.topkey[lane] = x;
-    if (lane == 0) sm.ntop = (tied > inset) ? -1 : K;
   }
-  __syncthreads();
-  return sm.ntop == K ? 1 : 0;
+  below = wave_max_u32(below);
+  uint64_t x = ((uint32_t)lane < m) ? sel[lane] : 0ull;
+  uint64_t y = (64u + (uint32_t)lane < m) ? sel[64 + lane] : 0ull;
+  wave_sort2(x, y);  // x descending, y ascending
+  const uint64_t lo = x > y ? y : x;
+  x = wave_merge<false>(x > y ? x : y);
+  // The reference keeps the top K; if the K-th value is shared by a stored
+  // key outside them (the (K+1)-th largest), which tied logits it keeps
+  // depends on its slot order.
+  const uint32_t vk = (uint32_t)(readlane64(x, K - 1) >> 32);
+  uint32_t nextv;
+  if ((uint32_t)K < m)
+    nextv = (K < 64) ? (uint32_t)(readlane64(x, K) >> 32) : (uint32_t)(wave_max_u64(lo) >> 32);
+  else
+    nextv = below;
+  if (lane < K) sm.topkey[lane] = x;
+  if (lane == 0) sm.ntop = (nextv == vk) ? -1 : K;
+  return 1;
 }
+
 
 // Merge (the last workgroup of the row).  One round trip loads the chunk
 // records and, speculatively, the first kMergeSpec * kBlock candidate slots.
@@ -1511,7 +1573,15 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
     sm.replay = 1;
   }
   __syncthreads();
-  int mr = (S <= kFastChunks) ? topk_merge_waves(p.vocab, S, K, cm, cr, sm) : -1;
+  int mr = -1;
+  if (S <= kFastChunks) {
+    // wave 0 finishes the fast merge alone; its verdict is shared at the barrier
+    const int r = topk_merge_waves(p.vocab, S, K, cm, cr, sm);
+    if (threadIdx.x == 0) sm.mres = (r == 2) ? 0 : r;
+    __syncthreads();
+    mr = sm.mres;
+    if (mr > 0) mr = (sm.ntop == K) ? 1 : 0;
+  }
   if (p.fuse_penalty) {
     penalty_write_back(p, row, pf, gx, sm);
     if (mr <= 0) {  // the paths below re-read the row: the stores must be visible
