@@ -216,6 +216,87 @@ def run_gpu(name, steps, warmup, eager):
                 replay_frac=float(((flags & 0x4) != 0).mean()))
 
 
+LMHEAD_V, LMHEAD_D = 262144, 2560  # Gemma-3-4B tied lm_head (token_embd.weight)
+VALU_FP32_PEAK_TFLOPS = 157.3      # MI355X published FP32 vector peak (packed FMA)
+
+
+def run_lmhead(B, steps, warmup):
+    """lm_head + sampling with the logits kept in HBM (RunUnembedding followed
+    by Process, Inference.pas:327-339): the Q4_0 lm_head of 262144 x 2560
+    (nibbles uniform 0..15, fp16 scales |N(0, 0.02)|) over B hidden rows
+    N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  Times the whole call (both
+    kernels) and the lm_head kernel alone, each from a captured hipGraph."""
+    import torch
+
+    from vindexllm_amd import TVdxSampler, lmhead_q4_0
+
+    V, D = LMHEAD_V, LMHEAD_D
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1005)
+    nb = D // 32
+    w = torch.randint(0, 256, (V, nb, 18), dtype=torch.uint8, device=dev, generator=g)
+    d = (torch.randn(V, nb, device=dev, generator=g) * 0.02).abs().half()
+    w[:, :, 0:2] = d.view(torch.uint8).view(V, nb, 2)
+    w = w.view(-1)
+    hidden = torch.randn(B, D, device=dev, generator=g)
+    logits = torch.empty(B, V, dtype=torch.float32, device=dev)
+    scratch = torch.empty(16 * D, dtype=torch.float32, device=dev)
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    s = TVdxSampler(0, B)
+    c = s.DefaultConfig()
+    c.Temperature, c.TopK, c.TopP, c.Seed = 1.0, 64, 0.95, 3005
+    s.SetConfig(c)
+    cs = torch.cuda.Stream(dev)
+    cs.wait_stream(torch.cuda.current_stream(dev))
+
+    def both():
+        s.lmhead_q4_0_device(w, hidden, V, logits=logits, tokens=tok, stream=cs)
+
+    def head():
+        lmhead_q4_0(w, hidden, V, logits=logits, scratch=scratch, stream=cs)
+
+    res = {}
+    for tag, fn in (("call", both), ("lmhead", head)):
+        with torch.cuda.stream(cs):
+            for _ in range(max(warmup, 1)):
+                fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cs):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        # replay() launches on torch's current stream: the events go there
+        rs = torch.cuda.current_stream(dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(rs)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(rs)
+        torch.cuda.synchronize()
+        res[tag] = dict(wall_us=1e6 * (time.perf_counter() - t0) / steps,
+                        event_us=1e3 * e0.elapsed_time(e1) / steps)
+    s.Free()
+    head_us = res["lmhead"]["event_us"]
+    weight_bytes = V * nb * 18
+    alg_bytes = weight_bytes + B * D * 4
+    flops = 2.0 * V * D * B
+    out = {"rows_per_s": B / (res["call"]["wall_us"] * 1e-6),
+           "us_per_step": res["call"]["wall_us"],
+           "call_event_us": res["call"]["event_us"],
+           "lmhead_kernel_us": head_us,
+           "lmhead_gbs": alg_bytes / (head_us * 1e-6) / 1e9,
+           "lmhead_hbm_frac": alg_bytes / (head_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "lmhead_tflops": flops / (head_us * 1e-6) / 1e12,
+           "lmhead_valu_frac": flops / (head_us * 1e-6) / 1e12 / VALU_FP32_PEAK_TFLOPS,
+           "bound": "hbm" if B == 1 else "valu",
+           "desc": f"Q4_0 lm_head {V}x{D} + top-k 64/top-p 0.95, B={B} hidden rows N(0,1)"}
+    return out
+
+
 def copy_calibration(nbytes=1 << 30, reps=5):
     """Device-to-device copies of a known size, for scaling rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
@@ -302,6 +383,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--others", action="store_true", help="also measure the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--lmhead", type=int, metavar="B",
+                    help="only the Q4_0 lm_head + sampling workload at B hidden rows (one JSON line)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU: turn two rocprofv3 --pmc counter CSVs into profiles/traffic_<workload>.json")
     a = ap.parse_args()
@@ -313,6 +396,9 @@ def main():
               "collective (rows shard with zero exchange), so --gpus must be 1", file=sys.stderr)
         sys.exit(3)
 
+    if a.lmhead:
+        print(json.dumps(run_lmhead(a.lmhead, min(a.steps, 500), min(a.warmup, 20))), flush=True)
+        return
     r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
     ms_step = 1e3 * r["elapsed"] / r["steps"]
@@ -353,6 +439,8 @@ def main():
                             "kernel_us": 1e3 * o["kernel_ms"],
                             "kernel_hbm_frac": o["step_bytes"] / (o["kernel_ms"] * 1e-3) / 1e9
                             / HBM_PEAK_GBS}
+        for B in (1, 16):
+            others[f"lmhead_b{B}"] = run_lmhead(B, 200, 10)
         out["other_workloads"] = others
     if a.copy_calibration:
         copy_calibration()

@@ -889,13 +889,16 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
 // Fast merge for rows of at most kFastChunks chunks, with no block-wide
 // compaction: every wave reads the chunk records itself (T = max tau_c) and
 // filters the candidate slots of chunks wv, wv+4, ... (loaded in the same round
-// trip as the records) against T into its own LDS list, sorts it in registers
-// (descending in waves 0 and 2, ascending in 1 and 3), and the four sorted
-// lists merge pairwise by lane-wise maxima and bitonic merges.  Returns 1 when
-// sm.topkey holds the row's top K, 0 when the row must be replayed (NaN/+inf,
-// or the K-th value tied with a stored key outside the set), -1 when the
-// general merge must run (a region overflowed, fewer than K keys reach T, or a
-// wave list would exceed kWaveCand).
+// trip as the records) against T into its own LDS list.  Wave 0 then narrows
+// the lists with one 8-bit radix digit to the at most 128 keys that can be in
+// the top K, sorts them with two interleaved in-register networks and one
+// bitonic merge.  Returns 1 in wave 0 when sm.topkey holds the row's top K
+// (sm.ntop = -1 when the K-th value is tied with a stored key outside the
+// set: replay), 2 in waves 1-3 (they learn wave 0's result through LDS after
+// the caller's barrier), 0 when the row must be replayed (NaN/+inf), and -1
+// when the general merge must run (a region overflowed, fewer than K keys
+// reach T, a wave list would exceed kWaveCand, or more than 128 keys survive
+// the digit).
 constexpr int kFastChunks = 16;
 constexpr int kWaveCand = 256;
 static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMergeCap && kBlock == 256,
