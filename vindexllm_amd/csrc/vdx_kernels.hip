@@ -104,15 +104,18 @@ __device__ __forceinline__ void load_chunk(const float *__restrict__ base, int c
 // workgroup that finished the row last.  Records written with xstore() before
 // the call by any workgroup of the row are complete when the winner reads them
 // with xload(): each wave waits for its stores to be acknowledged before the
-// workgroup takes its ticket.
-__device__ __forceinline__ bool last_of_row(uint32_t *tickets, int row, int nchunks, int *flag) {
+// workgroup takes its ticket.  `meanwhile()` runs (in every thread) while the
+// ticket is in flight.
+template <typename F>
+__device__ __forceinline__ bool last_of_row(uint32_t *tickets, int row, int nchunks, int *flag,
+                                            F &&meanwhile) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t t = __hip_atomic_fetch_add(&tickets[row], 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_SYSTEM);
-    *flag = (t == (uint32_t)(nchunks - 1));
-  }
+  uint32_t t = 0u;
+  if (threadIdx.x == 0)
+    t = __hip_atomic_fetch_add(&tickets[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  meanwhile();
+  if (threadIdx.x == 0) *flag = (t == (uint32_t)(nchunks - 1));
   __syncthreads();
   if (!*flag) return false;
   if (threadIdx.x == 0)  // every other chunk has arrived: reset for the next launch
@@ -133,6 +136,26 @@ __device__ __forceinline__ float penalise(float x, int k, float pen) {
       x = x / pen;
     else if (x < 0.0f)
       x = x * pen;
+  }
+  return x;
+}
+
+// The same k steps with the division as a double product: for fp32 x and p
+// (normal, p > 0) with ip = RN64(1/p), RN32(RN64(x * ip)) = RN32(x / p)
+// whenever that quotient is normal.  RN64(x * ip) is within 2^-52 (relative)
+// of x / p, while x / p is never within 2^-49 of a midpoint of two fp32 values
+// (with x = A 2^a, p = B 2^b, A, B < 2^24, and a midpoint m = M 2^c, M odd,
+// 2^24 <= M < 2^25: x - m p is a non-zero multiple of 2^min(a, b + c), as M B
+// has more than 24 significant bits), so both round to the same fp32 value.
+// Quotients below 2^-125 (subnormal or close to it) take the IEEE division.
+__device__ __forceinline__ float penalise_fast(float x, int k, float pen, double ip) {
+  for (int r = 0; r < k; ++r) {
+    if (x > 0.0f) {
+      const double q = (double)x * ip;
+      x = (q >= 0x1p-125) ? (float)q : x / pen;
+    } else if (x < 0.0f) {
+      x = x * pen;
+    }
   }
   return x;
 }
@@ -223,7 +246,7 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
     for (int w = 1; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
     xstore(&p.gpart[(int64_t)row * p.nchunks + chunk], k);
   }
-  if (!last_of_row(p.tickets, row, p.nchunks, &s_last)) return;
+  if (!last_of_row(p.tickets, row, p.nchunks, &s_last, [] {})) return;
   uint64_t k = 0;
   for (int c = tid; c < p.nchunks; c += kBlock) {
     const uint64_t x = xload(&p.gpart[(int64_t)row * p.nchunks + c]);
@@ -267,7 +290,7 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
 constexpr int kMergeSpec = 8;   // candidate slots loaded per thread per round
 constexpr int kMergeTop = 512;  // keys >= T handled by the bitonic merge
 
-constexpr int kPenHash = 2 * kPenMax;  // open-addressing table of the fused penalty
+constexpr int kPenHash = 8 * kPenMax;  // open-addressing table of the fused penalty
 
 struct TopkSmem {
   uint32_t thr[64];
@@ -303,10 +326,11 @@ struct TopkSmem {
   float q_ord[kKMax];
   int32_t i_ord[kKMax];
   float v_ord[kKMax];
-  // fused penalty: the row's history ids, one entry per distinct id
-  int32_t hid[kPenHash];     // id, or -1
-  uint32_t hcnt[kPenHash];   // occurrences in the history
-  int32_t hfirst[kPenHash];  // first history slot holding the id
+  // fused penalty: one entry per distinct history id, id | occurrences << 22
+  uint32_t ptab[kPenHash];
+  int32_t pid[64];  // wave 0's history ids (-1: none) and gathered logits
+  float pgx[64];
+  uint64_t pstage[kWaves][64];  // per-wave staging of the keys to penalise
   union {
     uint64_t sk[kMergeCap];
     struct {
@@ -334,114 +358,188 @@ __device__ __forceinline__ int chunk_quota(int K, int S) {
 }
 
 // Repetition penalty fused into the top-K kernel (Sampler.pas:285-303), for
-// penalties > 1 (which never raise a logit: x > 0 -> x / p < x, x < 0 ->
-// x * p < x).  Every workgroup of the row loads the row's history before its
-// chunk and, while the chunk is still in flight, counts the ids in an LDS
-// open-addressing table.  The stream phase selects candidates on the
-// unpenalised values -- a logit that is not stored is below tau_c before the
-// penalty, so also after it -- and gives every stored candidate whose index is
-// in the table its penalised value (the reference's sign test and divide /
-// multiply once per occurrence).  The row's last workgroup gathers the logits
-// at all history ids in the same round trip as the candidates and writes the
-// penalised values in place (the reference mutates its input).
+// penalties > 1, which never raise a logit (x > 0 -> x / p < x, x < 0 ->
+// x * p < x).  The stream phase selects and stores candidates on the
+// unpenalised values: a logit that is not stored is below tau_c before the
+// penalty, so also after it, and the merge's exactness argument holds for the
+// penalised values of the stored keys.  Every workgroup only prefetches the
+// row's history ids (one per thread); the row's last workgroup gathers the
+// logits at those ids right after its ticket, counts the ids in an LDS table
+// while the chunk records are in flight, gives every stored key whose index
+// is in the table its penalised value (the reference's sign test and divide /
+// multiply once per occurrence) before the merge ranks the keys, and writes
+// the penalised logits back in place (the reference mutates its input) from
+// waves 1-3 while wave 0 finishes the merge (wave 0 hands its ids and
+// gathered logits to wave 1 through LDS).
 constexpr int kPenPerThread = kPenMax / kBlock;
+static_assert(kPenPerThread == 1, "one history id per thread");
+constexpr uint32_t kPenEmpty = 0xFFFFFFFFu;
+constexpr uint32_t kPenIdMask = (1u << 22) - 1u;  // ids < 4 Mi; count in the top 10 bits
+static_assert(kMaxChunks * kChunk <= (1 << 22) && kPenMax < 1024, "packed penalty table entries");
+static_assert(kPenMax < kPenHash, "an occurrence count is also a valid table index");
 
 struct PenaltyPrefetch {
   int cnt;
   int32_t id[kPenPerThread];
 };
 
+// History position of prefetched id r of this thread.
+__device__ __forceinline__ int pen_pos(int r) { return (int)threadIdx.x + r * kBlock; }
+
+__device__ __forceinline__ bool pen_valid(const CallParams &p, const PenaltyPrefetch &pf, int r) {
+  const int t = pen_pos(r);
+  return t < min(pf.cnt, p.hist_len) && pf.id[r] >= 0 && pf.id[r] < p.vocab;
+}
+
 __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
   const int W = p.hist_len;
   const int32_t *h = p.hist + (int64_t)row * W;
   pf.cnt = p.rng.rows[row].hist_count;
-  // Unconditional loads (index clamped; slots t >= count are ignored where the
-  // ids are used), and no arithmetic on them here: the chunk's loads are
+  // Unconditional loads (index clamped; invalid positions are ignored where
+  // the ids are used), and no arithmetic on them here: the chunk's loads are
   // issued before anything waits for the ids.
 #pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) pf.id[r] = h[min((int)threadIdx.x + r * kBlock, W - 1)];
+  for (int r = 0; r < kPenPerThread; ++r) pf.id[r] = h[min(pen_pos(r), W - 1)];
 }
 
-__device__ __forceinline__ uint32_t pen_hash(int32_t id) {
-  return ((uint32_t)id * 2654435761u) >> (32 - 9);  // kPenHash = 512 slots
+__device__ __forceinline__ uint32_t pen_hash(uint32_t id) {
+  return (id * 2654435761u) >> (32 - 11);  // kPenHash = 2048 slots
 }
-static_assert(kPenHash == 512, "pen_hash yields 9 bits");
+static_assert(kPenHash == 2048, "pen_hash yields 11 bits");
 
-// Builds the table from the prefetched ids (two barriers; the chunk's loads
-// stay in flight).
+// Counts the prefetched ids in the open-addressing table: entry = id | count
+// << 22, kPenEmpty if free; at most kPenMax distinct ids in kPenHash slots, so
+// a free slot always exists.  Two barriers.
 __device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, TopkSmem &sm) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < kPenHash; i += kBlock) {
-    sm.hid[i] = -1;
-    sm.hcnt[i] = 0u;
-    sm.hfirst[i] = 0x7FFFFFFF;
-  }
+#pragma unroll
+  for (int i = 0; i < kPenHash / kBlock; ++i) sm.ptab[threadIdx.x + i * kBlock] = kPenEmpty;
   __syncthreads();
-  const int cnt = min(pf.cnt, p.hist_len);
 #pragma unroll
   for (int r = 0; r < kPenPerThread; ++r) {
-    const int t = tid + r * kBlock;
-    const int id = pf.id[r];
-    if (t < cnt && id >= 0 && id < p.vocab) {
+    if (pen_valid(p, pf, r)) {
+      const uint32_t id = (uint32_t)pf.id[r];
       uint32_t h = pen_hash(id);
-      for (;;) {  // at most cnt <= kPenHash / 2 distinct ids: a free slot exists
-        const int old = atomicCAS(&sm.hid[h], -1, id);
-        if (old == -1 || old == id) break;
+      for (;;) {
+        const uint32_t old = atomicCAS(&sm.ptab[h], kPenEmpty, id | (1u << 22));
+        if (old == kPenEmpty) break;
+        if ((old & kPenIdMask) == id) {
+          atomicAdd(&sm.ptab[h], 1u << 22);
+          break;
+        }
         h = (h + 1u) & (uint32_t)(kPenHash - 1);
       }
-      atomicAdd(&sm.hcnt[h], 1u);
-      atomicMin(&sm.hfirst[h], t);
     }
   }
   __syncthreads();
 }
 
-// Slot of `id` in the table, or -1.
-__device__ __forceinline__ int pen_find(const TopkSmem &sm, int32_t id) {
+// Occurrences of `id` in the history (0 if none).
+__device__ __forceinline__ uint32_t pen_count(const TopkSmem &sm, uint32_t id) {
   uint32_t h = pen_hash(id);
-  for (int n = 0; n < kPenHash; ++n) {
-    const int32_t e = sm.hid[h];
-    if (e == id) return (int)h;
-    if (e == -1) return -1;
+  for (;;) {
+    const uint32_t e = sm.ptab[h];
+    if (e == kPenEmpty) return 0u;
+    if ((e & kPenIdMask) == id) return e >> 22;
     h = (h + 1u) & (uint32_t)(kPenHash - 1);
   }
-  return -1;
 }
 
-// The value the reference's penalty leaves at index `id` (x before it).
-__device__ __forceinline__ float pen_value(const CallParams &p, const TopkSmem &sm, int32_t id, float x) {
-  const int h = pen_find(sm, id);
-  return (h < 0) ? x : penalise(x, (int)sm.hcnt[h], p.penalty);
+// Keys k[s] with bit s of `need` set get the penalised value if their index
+// is a history id.  The table probes of all N keys advance together (one LDS
+// read per key per round, issued back to back); the keys that are history ids
+// are then compacted across the wave into sm.pstage, so each lane runs at
+// most one divide / multiply chain, and read back.
+template <int N>
+__device__ __forceinline__ void pen_fix_keys(const CallParams &p, TopkSmem &sm, uint64_t (&k)[N],
+                                             uint32_t need) {
+  const int lane = lane_id(), wv = threadIdx.x >> 6;
+  uint32_t h[N];  // probe slot while pending, then the occurrence count
+#pragma unroll
+  for (int s = 0; s < N; ++s) h[s] = pen_hash(~(uint32_t)k[s]);
+  uint32_t pend = need, hit = 0u;
+  while (__ballot(pend != 0u)) {
+    uint32_t e[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s) e[s] = sm.ptab[h[s] & (uint32_t)(kPenHash - 1)];
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      if ((pend >> s) & 1u) {
+        if (e[s] == kPenEmpty) {
+          pend &= ~(1u << s);
+        } else if ((e[s] & kPenIdMask) == ~(uint32_t)k[s]) {
+          h[s] = e[s] >> 22;
+          hit |= 1u << s;
+          pend &= ~(1u << s);
+        } else {
+          h[s] = (h[s] + 1u) & (uint32_t)(kPenHash - 1);
+        }
+      }
+    }
+  }
+  const uint32_t nh = (uint32_t)__popc(hit);
+  const uint32_t incl = wave_incl_scan_u32(nh);
+  const uint32_t tot = readlane32(incl, 63);
+  uint64_t *st = sm.pstage[wv];
+  for (uint32_t base = 0u; base < tot; base += 64u) {  // uniform
+    uint32_t q = incl - nh;
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      if ((hit >> s) & 1u) {
+        if (q - base < 64u) st[q - base] = (k[s] & 0xFFFFFFFF00000000ull) | h[s];
+        ++q;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if ((uint32_t)lane < tot - base) {
+      const uint64_t v = st[lane];
+      const float x = penalise_fast(key_float((uint32_t)(v >> 32)), (int)(uint32_t)v, p.penalty,
+                                    1.0 / (double)p.penalty);
+      st[lane] = (uint64_t)ord_key(x) << 32;
+    }
+    __builtin_amdgcn_wave_barrier();
+    q = incl - nh;
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      if ((hit >> s) & 1u) {
+        if (q - base < 64u) k[s] = (st[q - base] & 0xFFFFFFFF00000000ull) | (uint32_t)k[s];
+        ++q;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
 }
 
-// Last workgroup of the row: the logits at the history ids (gathered before
-// the merge) are penalised once per distinct id and stored in place.
+// Last workgroup of the row: the logits at the history ids (gathered right
+// after the ticket) are penalised and stored in place.  A repeated id is
+// stored once per occurrence, always with the same value.  `handoff`: wave 1
+// also stores wave 0's positions, which wave 0 left in sm.pid / sm.pgx.
 __device__ __forceinline__ void penalty_write_back(const CallParams &p, int row, const PenaltyPrefetch &pf,
-                                                   const float (&gx)[kPenPerThread], const TopkSmem &sm) {
+                                                   const float (&gx)[kPenPerThread], const TopkSmem &sm,
+                                                   bool handoff) {
   float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
-  const int cnt = min(pf.cnt, p.hist_len);
+  const double ip = 1.0 / (double)p.penalty;
 #pragma unroll
   for (int r = 0; r < kPenPerThread; ++r) {
-    const int t = threadIdx.x + r * kBlock;
-    const int id = pf.id[r];
-    if (t < cnt && id >= 0 && id < p.vocab) {
-      const int h = pen_find(sm, id);
-      if (h >= 0 && sm.hfirst[h] == t) xstoref(&Lw[id], penalise(gx[r], (int)sm.hcnt[h], p.penalty));
+    if (pen_valid(p, pf, r)) {
+      const uint32_t id = (uint32_t)pf.id[r];
+      xstoref(&Lw[id], penalise_fast(gx[r], (int)pen_count(sm, id), p.penalty, ip));
     }
+  }
+  if (handoff && (threadIdx.x >> 6) == 1) {
+    const int32_t id = sm.pid[threadIdx.x - 64];
+    if (id >= 0)
+      xstoref(&Lw[id], penalise_fast(sm.pgx[threadIdx.x - 64], (int)pen_count(sm, (uint32_t)id), p.penalty, ip));
   }
 }
 
 template <bool VEC>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
-                                            ChunkMeta *__restrict__ meta, const PenaltyPrefetch &pf,
-                                            TopkSmem &sm) {
+                                            ChunkMeta *__restrict__ meta, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
-  const bool pen = p.fuse_penalty != 0;
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
-  if (pen) penalty_table(p, pf, sm);
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
@@ -481,7 +579,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   } else if (clen > kCandCap) {
     // the largest of 64 sampled thread maxima (wave 0's) that >= Kq reach
     uint32_t mycnt = 0u;
-#pragma unroll 8
+#pragma unroll 4
     for (int j = 0; j < 64; ++j) {
       const uint32_t tj = sm.thr[j];
       const uint32_t c = (uint32_t)__popcll(__ballot(mk >= tj));
@@ -517,8 +615,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
             const uint32_t q = wc + lane_rank(hb);
             if (hit && q < (uint32_t)cap) {
               const int idx = c0 + l0 + e;
-              const float x = pen ? pen_value(p, sm, idx, v[4 * j + e]) : v[4 * j + e];
-              xstore(&wreg[q], ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)idx));
+              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(~(uint32_t)idx));
             }
             wc += (uint32_t)__popcll(hb);
           }
@@ -539,8 +636,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
             const uint32_t q = wc + lane_rank(hb);
             if (hit && q < (uint32_t)cap) {
               const int idx = c0 + l0 + e;
-              const float x = pen ? pen_value(p, sm, idx, v[4 * j + e]) : v[4 * j + e];
-              xstore(&wreg[q], ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)idx));
+              xstore(&wreg[q], ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(~(uint32_t)idx));
             }
             wc += (uint32_t)__popcll(hb);
           }
@@ -743,9 +839,11 @@ __device__ __forceinline__ int last_region_sh(int V, int S) {
 // and theta is recomputed.  Returns false when the row must be replayed: LDS
 // capacity exceeded, or the K-th value tied with a logit outside the set.
 template <bool VEC>
-__device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, int V, int S, int K,
+__device__ __forceinline__ bool topk_merge_general(const CallParams &p, const float *__restrict__ L, int S,
                                                    const Cand *__restrict__ cand_row, TopkSmem &sm,
                                                    uint64_t (&kk)[kMergeSpec], bool reload) {
+  const int V = p.vocab, K = p.top_k;
+  const bool pen = p.fuse_penalty != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslots = S * kCandCap;
   const int last_sh = last_region_sh(V, S);
@@ -753,17 +851,23 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
   __syncthreads();
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
   for (int base = 0; base < nslots; base += kMergeSpec * kBlock) {
-    if (base > 0 || reload) {
+    if (base > 0 || reload || pen) {  // with the penalty: unpenalised keys, fresh
 #pragma unroll
       for (int r = 0; r < kMergeSpec; ++r) {
         const int i = base + tid + r * kBlock;
         kk[r] = (i < nslots) ? xload(&cand_row[i]) : 0ull;
       }
     }
+    uint32_t vm = 0u;
 #pragma unroll
     for (int r = 0; r < kMergeSpec; ++r) {
       const int i = base + tid + r * kBlock;
-      if (i < nslots && slot_valid(i, S, last_sh, sm)) {
+      vm |= (i < nslots && slot_valid(i, S, last_sh, sm)) ? (1u << r) : 0u;
+    }
+    if (pen) pen_fix_keys(p, sm, kk, vm);
+#pragma unroll
+    for (int r = 0; r < kMergeSpec; ++r) {
+      if ((vm >> r) & 1u) {
         const uint32_t q = atomicAdd(&sm.n, 1u);
         if (q < (uint32_t)kMergeCap) sm.buf.sk[q] = kk[r];
         kmin = min(kmin, (uint32_t)(kk[r] >> 32));
@@ -892,20 +996,27 @@ __device__ __forceinline__ bool topk_merge_general(const float *__restrict__ L, 
 // trip as the records) against T into its own LDS list.  Wave 0 then narrows
 // the lists with one 8-bit radix digit to the at most 128 keys that can be in
 // the top K, sorts them with two interleaved in-register networks and one
-// bitonic merge.  Returns 1 in wave 0 when sm.topkey holds the row's top K
-// (sm.ntop = -1 when the K-th value is tied with a stored key outside the
-// set: replay), 2 in waves 1-3 (they learn wave 0's result through LDS after
-// the caller's barrier), 0 when the row must be replayed (NaN/+inf), and -1
-// when the general merge must run (a region overflowed, fewer than K keys
-// reach T, a wave list would exceed kWaveCand, or more than 128 keys survive
-// the digit).
+// bitonic merge.  With the fused penalty the table of history ids is built
+// while the loads are in flight and the keys are penalised before the filter.
+// Before the filter barrier every wave returns the same code: 0 when the row
+// must be replayed (NaN/+inf), -1 when the general merge must run (a region
+// overflowed).  After it, waves 1-3 return 2 (they learn wave 0's result
+// through LDS after the caller's barrier) and wave 0 returns 1 when
+// sm.topkey holds the row's top K (sm.ntop = -1 when the K-th value is tied
+// with a stored key outside the set: replay) or -2 when the general merge
+// must run (fewer than K keys reach T, a wave list would exceed kWaveCand, or
+// more than 128 keys survive the digit).
 constexpr int kFastChunks = 16;
 constexpr int kWaveCand = 256;
 static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMergeCap && kBlock == 256,
               "fast merge buffers");
 
-__device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const ChunkMeta *__restrict__ cm,
+__device__ __forceinline__ int topk_merge_waves(const CallParams &p, const PenaltyPrefetch &pf,
+                                                const float (&gx)[kPenPerThread], int S,
+                                                const ChunkMeta *__restrict__ cm,
                                                 const Cand *__restrict__ cand_row, TopkSmem &sm) {
+  const int V = p.vocab, K = p.top_k;
+  const bool pen = p.fuse_penalty != 0;
   const int lane = lane_id(), wv = threadIdx.x >> 6;
   // one round trip: the records (lane c < S) and this wave's candidate slots
   const int lc = min(lane, S - 1);
@@ -932,26 +1043,66 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
 
   // keys >= T of this wave's chunks, compacted by ballot into its LDS list
   const uint64_t thr = (uint64_t)T << 32;
+  uint32_t okm = 0u;  // bit 2j+e: slot holds a stored key >= T
+#pragma unroll
+  for (int j = 0; j < kFastChunks / kWaves; ++j) {
+    const int c = wv + kWaves * j;
+    if (c < S) {  // uniform
+      const uint32_t cnt = readlane32(counts, c);
+      const uint32_t ccap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk));
+      const int sh = ccap == 128u ? 7 : (ccap == 64u ? 6 : 5);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t slot = 2u * (uint32_t)lane + (uint32_t)e;
+        const uint32_t have = (cnt >> (8 * (slot >> sh))) & 0xFFu;
+        okm |= ((slot & (ccap - 1u)) < have && kk[2 * j + e] >= thr) ? (1u << (2 * j + e)) : 0u;
+      }
+    }
+  }
+  if (pen && wv == 0) {  // wave 1 writes wave 0's penalised logits back
+    sm.pid[lane] = pen_valid(p, pf, 0) ? pf.id[0] : -1;
+    sm.pgx[lane] = gx[0];
+  }
   uint64_t *wl = sm.buf.sk + wv * kWaveCand;
   uint32_t nw = 0u, vmax_k = 0u;
 #pragma unroll
   for (int j = 0; j < kFastChunks / kWaves; ++j) {
-    const int c = wv + kWaves * j;
-    if (c >= S) break;  // uniform
-    const uint32_t cnt = readlane32(counts, c);
-    const uint32_t ccap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk));
-    const int sh = ccap == 128u ? 7 : (ccap == 64u ? 6 : 5);
+    if (wv + kWaves * j >= S) break;  // uniform
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const uint32_t slot = 2u * (uint32_t)lane + (uint32_t)e;
-      const uint32_t have = (cnt >> (8 * (slot >> sh))) & 0xFFu;
-      const bool ok = (slot & (ccap - 1u)) < have && kk[2 * j + e] >= thr;
+      const bool ok = (okm >> (2 * j + e)) & 1u;
       const uint64_t b = __ballot(ok);
       const uint32_t q = nw + lane_rank(b);
       if (ok && q < (uint32_t)kWaveCand) wl[q] = kk[2 * j + e];
       if (ok) vmax_k = max(vmax_k, (uint32_t)(kk[2 * j + e] >> 32));
       nw += (uint32_t)__popcll(b);
     }
+  }
+  // With the penalty, each lane penalises the list entries it owns (a key
+  // whose index is a history id); an entry that falls below T is cleared (it
+  // cannot be in the top K: at least K keys stay >= T, or the general merge
+  // runs) and no longer counted.
+  uint32_t live = nw;
+  if (pen) {
+    const double ip = 1.0 / (double)p.penalty;
+    const uint32_t nl = min(nw, (uint32_t)kWaveCand);
+    live = 0u;
+    vmax_k = 0u;
+    for (uint32_t i = (uint32_t)lane; i < nl; i += 64u) {
+      uint64_t k = wl[i];
+      const uint32_t c = pen_count(sm, ~(uint32_t)k);
+      if (c) {
+        k = ((uint64_t)ord_key(penalise_fast(key_float((uint32_t)(k >> 32)), (int)c, p.penalty, ip)) << 32) |
+            (uint32_t)k;
+        if (k < thr) k = 0ull;
+        wl[i] = k;
+      }
+      if (k >= thr) {
+        ++live;
+        vmax_k = max(vmax_k, (uint32_t)(k >> 32));
+      }
+    }
+    live = wave_sum_u32(live);
   }
   // Wave 0 alone from here: one radix digit (the highest bits in which T and
   // the largest key differ; the bits above are common to every key >= T)
@@ -962,6 +1113,7 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
   if (lane == 0) {
     sm.cnt[0][wv] = nw;
     sm.cnt[1][wv] = vmax_k;
+    sm.cnt[2][wv] = live;
   }
   sm.hist[threadIdx.x] = 0u;  // kBlock == 256 bins
   __syncthreads();
@@ -970,16 +1122,18 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
   bool big = false;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    nf += sm.cnt[0][w];
+    nf += sm.cnt[2][w];
     kmax = max(kmax, sm.cnt[1][w]);
     big = big || sm.cnt[0][w] > (uint32_t)kWaveCand;
   }
-  if (big || nf < (uint32_t)K || kmax == T) return -1;
+  if (big || nf < (uint32_t)K || kmax == T) return -2;
   const int shift = (31 - __clz((int)(T ^ kmax))) & ~7;
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < kWaves; ++w) {  // entries cleared by the penalty are skipped
     const uint32_t nw2 = sm.cnt[0][w];
-    for (uint32_t i = (uint32_t)lane; i < nw2; i += 64u)
-      atomicAdd(&sm.hist[(uint32_t)(sm.buf.sk[w * kWaveCand + i] >> (32 + shift)) & 255u], 1u);
+    for (uint32_t i = (uint32_t)lane; i < nw2; i += 64u) {
+      const uint64_t k = sm.buf.sk[w * kWaveCand + i];
+      if (k >= thr) atomicAdd(&sm.hist[(uint32_t)(k >> (32 + shift)) & 255u], 1u);
+    }
   }
   // bins from the top: lane l holds bins 255-4l .. 252-4l
   const int b0 = 255 - 4 * lane;
@@ -1000,7 +1154,7 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
     else if (e0 + g0 + g1 + g2 >= (uint32_t)K) { bstar = bb - 2u; m = e0 + g0 + g1 + g2; }
     else { bstar = bb - 3u; m = e0 + g0 + g1 + g2 + g3; }
   }
-  if (m > 128u) return -1;
+  if (m > 128u) return -2;
   // the m keys with digit >= bstar, and the largest value key below them
   uint64_t *sel = sm.buf.sk + kWaves * kWaveCand;
   uint32_t ns = 0u, below = 0u;
@@ -1009,7 +1163,7 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
     for (uint32_t i0 = 0u; i0 < nw2; i0 += 64u) {
       const uint32_t i = i0 + (uint32_t)lane;
       const uint64_t k = (i < nw2) ? sm.buf.sk[w * kWaveCand + i] : 0ull;
-      const bool in = i < nw2 && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
+      const bool in = i < nw2 && k >= thr && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
       const uint64_t bm = __ballot(in);
       if (in) sel[ns + lane_rank(bm)] = k;
       else if (i < nw2) below = max(below, (uint32_t)(k >> 32));
@@ -1047,9 +1201,11 @@ __device__ __forceinline__ int topk_merge_waves(int V, int S, int K, const Chunk
 // pairwise.  Otherwise, or when a wave's region overflowed, the general merge
 // runs.  Returns false when the row must be replayed.
 template <bool VEC>
-__device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, int S, int K,
+__device__ __forceinline__ bool topk_merge(const CallParams &p, const float *__restrict__ L, int S,
                                            const ChunkMeta *__restrict__ cm,
                                            const Cand *__restrict__ cand_row, TopkSmem &sm) {
+  const int V = p.vocab, K = p.top_k;
+  const bool pen = p.fuse_penalty != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslots = S * kCandCap;
   uint32_t fl = 0u, tmx = 0u;
@@ -1083,7 +1239,7 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
   fl = sm.cnt[1][0] | sm.cnt[1][1] | sm.cnt[1][2] | sm.cnt[1][3];
   tmx = max(max(sm.cnt[2][0], sm.cnt[2][1]), max(sm.cnt[2][2], sm.cnt[2][3]));
   if (fl) return false;
-  if (tmx == 0xFFFFFFFFu) return topk_merge_general<VEC>(L, V, S, K, cand_row, sm, kk, false);
+  if (tmx == 0xFFFFFFFFu) return topk_merge_general<VEC>(p, L, S, cand_row, sm, kk, false);
 
   // keys >= T, compacted by a block-wide exclusive scan
   const uint64_t thr = (uint64_t)tmx << 32;
@@ -1101,10 +1257,15 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
 #pragma unroll
     for (int r = 0; r < kMergeSpec; ++r) {
       const int i = base + tid + r * kBlock;
-      const bool ok = i < nslots && kk[r] >= thr && slot_valid(i, S, last_sh, sm);
-      vb |= ok ? (1u << r) : 0u;
-      m += ok ? 1u : 0u;
+      vb |= (i < nslots && kk[r] >= thr && slot_valid(i, S, last_sh, sm)) ? (1u << r) : 0u;
     }
+    if (pen) {  // penalised keys (this batch only: fresh loads each round)
+      pen_fix_keys(p, sm, kk, vb);
+#pragma unroll
+      for (int r = 0; r < kMergeSpec; ++r)
+        if (kk[r] < thr) vb &= ~(1u << r);
+    }
+    m = (uint32_t)__popc(vb);
     const uint32_t incl = wave_incl_scan_u32(m);
     if (lane == 63) sm.wtot[wv] = incl;
     __syncthreads();
@@ -1125,7 +1286,7 @@ __device__ __forceinline__ bool topk_merge(const float *__restrict__ L, int V, i
     __syncthreads();
   }
   if (nf < (uint32_t)K || nf > (uint32_t)kMergeTop)
-    return topk_merge_general<VEC>(L, V, S, K, cand_row, sm, kk, nslots > kMergeSpec * kBlock);
+    return topk_merge_general<VEC>(p, L, S, cand_row, sm, kk, pen || nslots > kMergeSpec * kBlock);
 
   // top 64 of the nf <= 512 keys
   uint64_t *R = sm.buf.sk + kMergeTop;  // four sorted lists of 64
@@ -1556,20 +1717,21 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
   RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
+  const bool pen = p.fuse_penalty != 0;
   PenaltyPrefetch pf;
-  if (p.fuse_penalty) penalty_prefetch(p, row, pf);  // issued before the chunk
+  if (pen) penalty_prefetch(p, row, pf);  // issued before the chunk
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
-                        cm + chunk, pf, sm);
-  if (!last_of_row(p.tickets, row, S, &sm.last)) return;
+                        cm + chunk, sm);
+  // with the penalty, every workgroup counts the history ids while its ticket
+  // is in flight (the winner needs the table; the others are done anyway)
+  if (!last_of_row(p.tickets, row, S, &sm.last, [&] {
+        if (pen) penalty_table(p, pf, sm);
+      }))
+    return;
   float gx[kPenPerThread];
-  if (p.fuse_penalty) {  // the logits at the history ids, gathered with the candidates
-    const int cnt = min(pf.cnt, p.hist_len);
+  if (pen) {  // the logits at the history ids, gathered before the merge's loads
 #pragma unroll
-    for (int r = 0; r < kPenPerThread; ++r) {
-      const int t = threadIdx.x + r * kBlock;
-      const int id = pf.id[r];
-      gx[r] = (t < cnt && id >= 0 && id < p.vocab) ? xloadf(&L[id]) : 0.0f;
-    }
+    for (int r = 0; r < kPenPerThread; ++r) gx[r] = pen_valid(p, pf, r) ? xloadf(&L[pf.id[r]]) : 0.0f;
   }
   if (threadIdx.x == 0) {
     sm.uval = rng_draw(p.rng, row, rp);
@@ -1577,22 +1739,24 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   }
   __syncthreads();
   int mr = -1;
+  bool written = false;  // penalised logits stored (not yet known to be visible)
   if (S <= kFastChunks) {
-    // wave 0 finishes the fast merge alone; its verdict is shared at the barrier
-    const int r = topk_merge_waves(p.vocab, S, K, cm, cr, sm);
-    if (threadIdx.x == 0) sm.mres = (r == 2) ? 0 : r;
+    // wave 0 finishes the fast merge alone while waves 1-3 write the
+    // penalised logits back; the verdict is shared at the barrier
+    const int r = topk_merge_waves(p, pf, gx, S, cm, cr, sm);
+    if (r == 2 && pen) penalty_write_back(p, row, pf, gx, sm, true);
+    if (threadIdx.x == 0) sm.mres = r;
     __syncthreads();
-    mr = sm.mres;
-    if (mr > 0) mr = (sm.ntop == K) ? 1 : 0;
+    const int m0 = sm.mres;
+    written = (m0 == 1 || m0 == -2);
+    mr = (m0 == 1) ? ((sm.ntop == K) ? 1 : 0) : (m0 == 0 ? 0 : -1);
   }
-  if (p.fuse_penalty) {
-    penalty_write_back(p, row, pf, gx, sm);
-    if (mr <= 0) {  // the paths below re-read the row: the stores must be visible
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
+  if (pen && (!written || mr < 0)) {  // the general merge re-reads the row: stores visible
+    if (!written) penalty_write_back(p, row, pf, gx, sm, false);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
-  if (mr < 0) mr = topk_merge<VEC>(L, p.vocab, S, K, cm, cr, sm) ? 1 : 0;
+  if (mr < 0) mr = topk_merge<VEC>(p, L, S, cm, cr, sm) ? 1 : 0;
   if (mr > 0) topk_fast(p, row, sm);
   if (sm.replay) {
     if (p.fuse_penalty) {  // the replay re-reads the row: the stores must be visible
@@ -1755,7 +1919,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
       xstore(&me->w[0], (uint64_t)__float_as_uint(base) | ((uint64_t)fc << 32));
     }
   }
-  if (!last_of_row(p.tickets, row, S, &sm.last)) return;
+  if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
 
   // ---- finish (last workgroup of the row) ----
   if (tid == 0) sm.u = rng_draw(p.rng, row, rp);
