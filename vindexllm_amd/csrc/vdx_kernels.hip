@@ -150,12 +150,10 @@ __device__ __forceinline__ float penalise(float x, int k, float pen) {
 // Quotients below 2^-125 (subnormal or close to it) take the IEEE division.
 __device__ __forceinline__ float penalise_fast(float x, int k, float pen, double ip) {
   for (int r = 0; r < k; ++r) {
-    if (x > 0.0f) {
-      const double q = (double)x * ip;
-      x = (q >= 0x1p-125) ? (float)q : x / pen;
-    } else if (x < 0.0f) {
-      x = x * pen;
-    }
+    const double q = (double)x * ip;
+    float d = (float)q;
+    if (x > 0.0f && !(q >= 0x1p-125)) d = x / pen;  // rare: tiny quotients
+    x = (x > 0.0f) ? d : ((x < 0.0f) ? x * pen : x);
   }
   return x;
 }
@@ -407,13 +405,16 @@ __device__ __forceinline__ uint32_t pen_hash(uint32_t id) {
 }
 static_assert(kPenHash == 2048, "pen_hash yields 11 bits");
 
-// Counts the prefetched ids in the open-addressing table: entry = id | count
-// << 22, kPenEmpty if free; at most kPenMax distinct ids in kPenHash slots, so
-// a free slot always exists.  Two barriers.
-__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, TopkSmem &sm) {
+// Empties the table (before a barrier that precedes penalty_table).
+__device__ __forceinline__ void penalty_table_clear(TopkSmem &sm) {
 #pragma unroll
   for (int i = 0; i < kPenHash / kBlock; ++i) sm.ptab[threadIdx.x + i * kBlock] = kPenEmpty;
-  __syncthreads();
+}
+
+// Counts the prefetched ids in the cleared open-addressing table: entry = id |
+// count << 22, kPenEmpty if free; at most kPenMax distinct ids in kPenHash
+// slots, so a free slot always exists.  One barrier.
+__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, TopkSmem &sm) {
 #pragma unroll
   for (int r = 0; r < kPenPerThread; ++r) {
     if (pen_valid(p, pf, r)) {
@@ -1008,7 +1009,8 @@ __device__ __forceinline__ bool topk_merge_general(const CallParams &p, const fl
 // more than 128 keys survive the digit).
 constexpr int kFastChunks = 16;
 constexpr int kWaveCand = 256;
-static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMergeCap && kBlock == 256,
+static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMergeCap && kBlock == 256 &&
+                  kWaveCand >= 128,
               "fast merge buffers");
 
 __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const PenaltyPrefetch &pf,
@@ -1118,23 +1120,32 @@ __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const Penal
   sm.hist[threadIdx.x] = 0u;  // kBlock == 256 bins
   __syncthreads();
   if (wv != 0) return 2;  // waves 1..3 wait at the final barrier of the caller
-  uint32_t nf = 0u, kmax = 0u;
+  uint32_t nf = 0u, kmax = 0u, nwl[kWaves];
   bool big = false;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
+    nwl[w] = sm.cnt[0][w];
     nf += sm.cnt[2][w];
     kmax = max(kmax, sm.cnt[1][w]);
-    big = big || sm.cnt[0][w] > (uint32_t)kWaveCand;
+    big = big || nwl[w] > 128u;
   }
   if (big || nf < (uint32_t)K || kmax == T) return -2;
   const int shift = (31 - __clz((int)(T ^ kmax))) & ~7;
-  for (int w = 0; w < kWaves; ++w) {  // entries cleared by the penalty are skipped
-    const uint32_t nw2 = sm.cnt[0][w];
-    for (uint32_t i = (uint32_t)lane; i < nw2; i += 64u) {
-      const uint64_t k = sm.buf.sk[w * kWaveCand + i];
-      if (k >= thr) atomicAdd(&sm.hist[(uint32_t)(k >> (32 + shift)) & 255u], 1u);
+  // the four lists in registers (entry 64j + lane of list w), all read at
+  // once; bit 2w+j of vm: a live key (entries cleared by the penalty are not)
+  uint64_t kv[kWaves][2];
+  uint32_t vm = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t i = 64u * (uint32_t)j + (uint32_t)lane;
+      kv[w][j] = sm.buf.sk[w * kWaveCand + i];
+      vm |= (i < nwl[w] && kv[w][j] >= thr) ? (1u << (2 * w + j)) : 0u;
     }
-  }
+#pragma unroll
+  for (int s = 0; s < 2 * kWaves; ++s)
+    if ((vm >> s) & 1u) atomicAdd(&sm.hist[(uint32_t)(kv[s >> 1][s & 1] >> (32 + shift)) & 255u], 1u);
   // bins from the top: lane l holds bins 255-4l .. 252-4l
   const int b0 = 255 - 4 * lane;
   const uint32_t h0 = sm.hist[b0], h1 = sm.hist[b0 - 1], h2 = sm.hist[b0 - 2], h3 = sm.hist[b0 - 3];
@@ -1158,17 +1169,15 @@ __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const Penal
   // the m keys with digit >= bstar, and the largest value key below them
   uint64_t *sel = sm.buf.sk + kWaves * kWaveCand;
   uint32_t ns = 0u, below = 0u;
-  for (int w = 0; w < kWaves; ++w) {
-    const uint32_t nw2 = sm.cnt[0][w];
-    for (uint32_t i0 = 0u; i0 < nw2; i0 += 64u) {
-      const uint32_t i = i0 + (uint32_t)lane;
-      const uint64_t k = (i < nw2) ? sm.buf.sk[w * kWaveCand + i] : 0ull;
-      const bool in = i < nw2 && k >= thr && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
-      const uint64_t bm = __ballot(in);
-      if (in) sel[ns + lane_rank(bm)] = k;
-      else if (i < nw2) below = max(below, (uint32_t)(k >> 32));
-      ns += (uint32_t)__popcll(bm);
-    }
+#pragma unroll
+  for (int s = 0; s < 2 * kWaves; ++s) {
+    const uint64_t k = kv[s >> 1][s & 1];
+    const bool v = (vm >> s) & 1u;
+    const bool in = v && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
+    const uint64_t bm = __ballot(in);
+    if (in) sel[ns + lane_rank(bm)] = k;
+    else if (v) below = max(below, (uint32_t)(k >> 32));
+    ns += (uint32_t)__popcll(bm);
   }
   below = wave_max_u32(below);
   uint64_t x = ((uint32_t)lane < m) ? sel[lane] : 0ull;
@@ -1719,7 +1728,10 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
   const bool pen = p.fuse_penalty != 0;
   PenaltyPrefetch pf;
-  if (pen) penalty_prefetch(p, row, pf);  // issued before the chunk
+  if (pen) {
+    penalty_prefetch(p, row, pf);  // issued before the chunk
+    penalty_table_clear(sm);       // the stream phase's barriers order it before the inserts
+  }
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
                         cm + chunk, sm);
   // with the penalty, every workgroup counts the history ids while its ticket
