@@ -230,10 +230,11 @@ def test_penalty_bitexact_and_repeats():
 
 
 def test_fused_penalty_paths():
-    # windows of <= 256 ids with penalties > 1 are applied inside the top-K
-    # kernel (candidates penalised, logits written back by the row's last
-    # workgroup); the fast merge, the replay (TopP = 1) and small K all see
-    # the penalised row, and the logits equal the reference's in-place result
+    # windows of <= 256 ids are applied inside the top-K kernel (each
+    # workgroup penalises the ids in its own chunk before selecting, and
+    # stores them in place); the fast merge, the replay (TopP = 1) and small K
+    # all see the penalised row, and the logits equal the reference's in-place
+    # result, for penalties above and below 1
     rng = np.random.default_rng(43)
     for V in (20000, 262144):
         B = 6
@@ -244,8 +245,10 @@ def test_fused_penalty_paths():
         hist = rng.integers(-5, V + 5, (B, 256)).astype(np.int32)
         hist[:, :60] = rng.choice(hot, (B, 60))   # repeats of the largest logits
         hist[:, 60:80] = 5
+        hist[1, :] = hot[0]                       # one id 256 times
+        hist[2, 100:140] = V - 1                  # the last (short) chunk's last logit
         u = u_stream(rng, B)
-        for p in (1.1, 3.0):
+        for p in (1.1, 3.0, 0.8):
             for k, tp in ((64, 0.9), (64, 1.0), (5, 0.5)):
                 _run(L, dict(temperature=1.0, top_k=k, top_p=tp, repeat_penalty=p,
                              repeat_window=256), u, hist=hist,

@@ -315,7 +315,7 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   // it itself for windows of up to kPenMax ids and penalties > 1 (which
   // never raise a logit); otherwise a separate kernel runs first
   const bool pen = c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0;
-  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax && c.repeat_penalty > 1.0f) ? 1 : 0;
+  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));

@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
 constexpr int kMergeSpec = 8;   // candidate slots loaded per thread per round
 constexpr int kMergeTop = 512;  // keys >= T handled by the bitonic merge
 
-constexpr int kPenHash = 8 * kPenMax;  // open-addressing table of the fused penalty
+constexpr int kPenHash = 4 * kPenMax;  // open-addressing table of the fused penalty
 
 struct TopkSmem {
   uint32_t thr[64];
@@ -326,9 +326,7 @@ struct TopkSmem {
   float v_ord[kKMax];
   // fused penalty: one entry per distinct history id, id | occurrences << 22
   uint32_t ptab[kPenHash];
-  int32_t pid[64];  // wave 0's history ids (-1: none) and gathered logits
-  float pgx[64];
-  uint64_t pstage[kWaves][64];  // per-wave staging of the keys to penalise
+  uint64_t pbits[kBlock];  // history positions among each thread's 64 logits
   union {
     uint64_t sk[kMergeCap];
     struct {
@@ -355,86 +353,78 @@ __device__ __forceinline__ int chunk_quota(int K, int S) {
   return min(K, max(8, q));
 }
 
-// Repetition penalty fused into the top-K kernel (Sampler.pas:285-303), for
-// penalties > 1, which never raise a logit (x > 0 -> x / p < x, x < 0 ->
-// x * p < x).  The stream phase selects and stores candidates on the
-// unpenalised values: a logit that is not stored is below tau_c before the
-// penalty, so also after it, and the merge's exactness argument holds for the
-// penalised values of the stored keys.  Every workgroup only prefetches the
-// row's history ids (one per thread); the row's last workgroup gathers the
-// logits at those ids right after its ticket, counts the ids in an LDS table
-// while the chunk records are in flight, gives every stored key whose index
-// is in the table its penalised value (the reference's sign test and divide /
-// multiply once per occurrence) before the merge ranks the keys, and writes
-// the penalised logits back in place (the reference mutates its input) from
-// waves 1-3 while wave 0 finishes the merge (wave 0 hands its ids and
-// gathered logits to wave 1 through LDS).
+// Repetition penalty fused into the top-K kernel (Sampler.pas:285-303): each
+// workgroup penalises the history ids that fall in its own chunk, in its
+// registers, before it selects anything, and stores those logits in place
+// (the reference mutates its input).  The ids are prefetched before the
+// chunk; while the chunk is in flight the in-chunk ids are counted in an LDS
+// open-addressing table (entry = id | occurrences << 22 over the whole
+// history) and marked in a per-thread bitmap of the positions each thread
+// holds.  Everything after (thread maxima, threshold, candidates, merge,
+// finish) then runs on penalised values, exactly as without a penalty, and
+// the stores are acknowledged before the workgroup takes its ticket, so the
+// row's last workgroup reads penalised logits wherever it re-reads the row.
 constexpr int kPenPerThread = kPenMax / kBlock;
 static_assert(kPenPerThread == 1, "one history id per thread");
 constexpr uint32_t kPenEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kPenIdMask = (1u << 22) - 1u;  // ids < 4 Mi; count in the top 10 bits
 static_assert(kMaxChunks * kChunk <= (1 << 22) && kPenMax < 1024, "packed penalty table entries");
-static_assert(kPenMax < kPenHash, "an occurrence count is also a valid table index");
+static_assert(kPerThread == 64, "one bit per position of a thread in a 64-bit mask");
 
 struct PenaltyPrefetch {
   int cnt;
   int32_t id[kPenPerThread];
 };
 
-// History position of prefetched id r of this thread.
-__device__ __forceinline__ int pen_pos(int r) { return (int)threadIdx.x + r * kBlock; }
-
-__device__ __forceinline__ bool pen_valid(const CallParams &p, const PenaltyPrefetch &pf, int r) {
-  const int t = pen_pos(r);
-  return t < min(pf.cnt, p.hist_len) && pf.id[r] >= 0 && pf.id[r] < p.vocab;
-}
-
 __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
   const int W = p.hist_len;
   const int32_t *h = p.hist + (int64_t)row * W;
   pf.cnt = p.rng.rows[row].hist_count;
-  // Unconditional loads (index clamped; invalid positions are ignored where
-  // the ids are used), and no arithmetic on them here: the chunk's loads are
-  // issued before anything waits for the ids.
-#pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) pf.id[r] = h[min(pen_pos(r), W - 1)];
+  // Unconditional load (index clamped; a position past the count is ignored
+  // where the id is used), and no arithmetic on it here: the chunk's loads
+  // are issued before anything waits for the id.
+  pf.id[0] = h[min((int)threadIdx.x, W - 1)];
 }
 
 __device__ __forceinline__ uint32_t pen_hash(uint32_t id) {
-  return (id * 2654435761u) >> (32 - 11);  // kPenHash = 2048 slots
+  return (id * 2654435761u) >> (32 - 10);  // kPenHash = 1024 slots
 }
-static_assert(kPenHash == 2048, "pen_hash yields 11 bits");
+static_assert(kPenHash == 1024, "pen_hash yields 10 bits");
 
-// Empties the table (before a barrier that precedes penalty_table).
-__device__ __forceinline__ void penalty_table_clear(TopkSmem &sm) {
+// Empties the table and the position bitmap (before a barrier).
+__device__ __forceinline__ void penalty_clear(TopkSmem &sm) {
 #pragma unroll
   for (int i = 0; i < kPenHash / kBlock; ++i) sm.ptab[threadIdx.x + i * kBlock] = kPenEmpty;
+  sm.pbits[threadIdx.x] = 0ull;
 }
 
-// Counts the prefetched ids in the cleared open-addressing table: entry = id |
-// count << 22, kPenEmpty if free; at most kPenMax distinct ids in kPenHash
-// slots, so a free slot always exists.  One barrier.
-__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, TopkSmem &sm) {
-#pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) {
-    if (pen_valid(p, pf, r)) {
-      const uint32_t id = (uint32_t)pf.id[r];
-      uint32_t h = pen_hash(id);
-      for (;;) {
-        const uint32_t old = atomicCAS(&sm.ptab[h], kPenEmpty, id | (1u << 22));
-        if (old == kPenEmpty) break;
-        if ((old & kPenIdMask) == id) {
-          atomicAdd(&sm.ptab[h], 1u << 22);
-          break;
-        }
-        h = (h + 1u) & (uint32_t)(kPenHash - 1);
+// Counts the history ids that fall in chunk [c0, c0 + clen) (at most kPenMax
+// distinct ids in kPenHash slots, so a free slot always exists) and marks
+// their positions: bit 4j + e of sm.pbits[64 wv + lane] is position
+// j*1024 + wv*256 + lane*4 + e (the interleaved chunk layout).
+__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, int c0, int clen,
+                                              TopkSmem &sm) {
+  const int t = threadIdx.x;
+  const int32_t id = pf.id[0];
+  if (t < min(pf.cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
+    const uint32_t uid = (uint32_t)id;
+    uint32_t h = pen_hash(uid);
+    for (;;) {
+      const uint32_t old = atomicCAS(&sm.ptab[h], kPenEmpty, uid | (1u << 22));
+      if (old == kPenEmpty) break;
+      if ((old & kPenIdMask) == uid) {
+        atomicAdd(&sm.ptab[h], 1u << 22);
+        break;
       }
+      h = (h + 1u) & (uint32_t)(kPenHash - 1);
     }
+    const int pos = id - c0;
+    atomicOr(&sm.pbits[((pos >> 8) & 3) * 64 + ((pos >> 2) & 63)],
+             1ull << (((pos >> 10) << 2) | (pos & 3)));
   }
-  __syncthreads();
 }
 
-// Occurrences of `id` in the history (0 if none).
+// Occurrences of `id` in the history (the id is in the table).
 __device__ __forceinline__ uint32_t pen_count(const TopkSmem &sm, uint32_t id) {
   uint32_t h = pen_hash(id);
   for (;;) {
@@ -445,102 +435,44 @@ __device__ __forceinline__ uint32_t pen_count(const TopkSmem &sm, uint32_t id) {
   }
 }
 
-// Keys k[s] with bit s of `need` set get the penalised value if their index
-// is a history id.  The table probes of all N keys advance together (one LDS
-// read per key per round, issued back to back); the keys that are history ids
-// are then compacted across the wave into sm.pstage, so each lane runs at
-// most one divide / multiply chain, and read back.
-template <int N>
-__device__ __forceinline__ void pen_fix_keys(const CallParams &p, TopkSmem &sm, uint64_t (&k)[N],
-                                             uint32_t need) {
-  const int lane = lane_id(), wv = threadIdx.x >> 6;
-  uint32_t h[N];  // probe slot while pending, then the occurrence count
+template <bool VEC>
+__device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
+                                            int c0, int clen, int Kq, Cand *__restrict__ cand,
+                                            ChunkMeta *__restrict__ meta, const PenaltyPrefetch &pf,
+                                            TopkSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int kG = kPerThread / 4;
+  const bool pen = p.fuse_penalty != 0;
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  if (pen) {  // while the chunk is in flight (the table was cleared at kernel start)
+    __syncthreads();
+    penalty_table(p, pf, c0, clen, sm);
+    __syncthreads();
+    const uint64_t hm = sm.pbits[tid];
+    __builtin_amdgcn_sched_barrier(0);
+    // the penalised logits at this thread's history positions, in registers
+    // and in place
+    if (__ballot(hm != 0ull)) {
+      float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
+      const double ip = 1.0 / (double)p.penalty;
 #pragma unroll
-  for (int s = 0; s < N; ++s) h[s] = pen_hash(~(uint32_t)k[s]);
-  uint32_t pend = need, hit = 0u;
-  while (__ballot(pend != 0u)) {
-    uint32_t e[N];
+      for (int j = 0; j < kG; ++j) {
+        const uint32_t nib = (uint32_t)(hm >> (4 * j)) & 15u;
+        if (__ballot(nib != 0u)) {
 #pragma unroll
-    for (int s = 0; s < N; ++s) e[s] = sm.ptab[h[s] & (uint32_t)(kPenHash - 1)];
-#pragma unroll
-    for (int s = 0; s < N; ++s) {
-      if ((pend >> s) & 1u) {
-        if (e[s] == kPenEmpty) {
-          pend &= ~(1u << s);
-        } else if ((e[s] & kPenIdMask) == ~(uint32_t)k[s]) {
-          h[s] = e[s] >> 22;
-          hit |= 1u << s;
-          pend &= ~(1u << s);
-        } else {
-          h[s] = (h[s] + 1u) & (uint32_t)(kPenHash - 1);
+          for (int e = 0; e < 4; ++e) {
+            if ((nib >> e) & 1u) {
+              const int idx = c0 + chunk_pos(wv, lane, 4 * j + e);
+              const float x = penalise_fast(v[4 * j + e], (int)pen_count(sm, (uint32_t)idx), p.penalty, ip);
+              v[4 * j + e] = x;
+              xstoref(&Lw[idx], x);
+            }
+          }
         }
       }
     }
   }
-  const uint32_t nh = (uint32_t)__popc(hit);
-  const uint32_t incl = wave_incl_scan_u32(nh);
-  const uint32_t tot = readlane32(incl, 63);
-  uint64_t *st = sm.pstage[wv];
-  for (uint32_t base = 0u; base < tot; base += 64u) {  // uniform
-    uint32_t q = incl - nh;
-#pragma unroll
-    for (int s = 0; s < N; ++s) {
-      if ((hit >> s) & 1u) {
-        if (q - base < 64u) st[q - base] = (k[s] & 0xFFFFFFFF00000000ull) | h[s];
-        ++q;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    if ((uint32_t)lane < tot - base) {
-      const uint64_t v = st[lane];
-      const float x = penalise_fast(key_float((uint32_t)(v >> 32)), (int)(uint32_t)v, p.penalty,
-                                    1.0 / (double)p.penalty);
-      st[lane] = (uint64_t)ord_key(x) << 32;
-    }
-    __builtin_amdgcn_wave_barrier();
-    q = incl - nh;
-#pragma unroll
-    for (int s = 0; s < N; ++s) {
-      if ((hit >> s) & 1u) {
-        if (q - base < 64u) k[s] = (st[q - base] & 0xFFFFFFFF00000000ull) | (uint32_t)k[s];
-        ++q;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
-}
-
-// Last workgroup of the row: the logits at the history ids (gathered right
-// after the ticket) are penalised and stored in place.  A repeated id is
-// stored once per occurrence, always with the same value.  `handoff`: wave 1
-// also stores wave 0's positions, which wave 0 left in sm.pid / sm.pgx.
-__device__ __forceinline__ void penalty_write_back(const CallParams &p, int row, const PenaltyPrefetch &pf,
-                                                   const float (&gx)[kPenPerThread], const TopkSmem &sm,
-                                                   bool handoff) {
-  float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
-  const double ip = 1.0 / (double)p.penalty;
-#pragma unroll
-  for (int r = 0; r < kPenPerThread; ++r) {
-    if (pen_valid(p, pf, r)) {
-      const uint32_t id = (uint32_t)pf.id[r];
-      xstoref(&Lw[id], penalise_fast(gx[r], (int)pen_count(sm, id), p.penalty, ip));
-    }
-  }
-  if (handoff && (threadIdx.x >> 6) == 1) {
-    const int32_t id = sm.pid[threadIdx.x - 64];
-    if (id >= 0)
-      xstoref(&Lw[id], penalise_fast(sm.pgx[threadIdx.x - 64], (int)pen_count(sm, (uint32_t)id), p.penalty, ip));
-  }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
-                                            int c0, int clen, int Kq, Cand *__restrict__ cand,
-                                            ChunkMeta *__restrict__ meta, TopkSmem &sm) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  constexpr int kG = kPerThread / 4;
-  float v[kPerThread];
-  load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
@@ -724,9 +656,12 @@ __device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, TopkSmem &sm, u
 // shifts by 4 in both directions (xor 4), DPP row_ror:8 (xor 8), and gfx950's
 // v_permlane16_swap / v_permlane32_swap (xor 16, 32), so a compare-exchange
 // step never waits on the LDS crossbar.
+// Lane-mask constants as per-lane conditions: the mask stays in an SGPR pair
+// and feeds v_cndmask directly (no per-lane compare).
+__device__ __forceinline__ bool lanes_in(uint64_t mask) { return __builtin_amdgcn_inverse_ballot_w64(mask); }
+
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane32(uint32_t v) {
-  const int l = lane_id();
   if constexpr (J == 1) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
   } else if constexpr (J == 2) {
@@ -734,17 +669,17 @@ __device__ __forceinline__ uint32_t xor_lane32(uint32_t v) {
   } else if constexpr (J == 4) {
     const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);  // lane + 4
     const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);  // lane - 4
-    return (l & 4) ? dn : up;
+    return lanes_in(0xF0F0F0F0F0F0F0F0ull) ? dn : up;  // lanes with bit 4 set
   } else if constexpr (J == 8) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
   } else if constexpr (J == 16) {
     // swap(v, v): first = rows {0,0,2,2}, second = rows {1,1,3,3}
     const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    return (l & 16) ? r[0] : r[1];
+    return lanes_in(0xFFFF0000FFFF0000ull) ? r[0] : r[1];  // lanes with bit 16 set
   } else {
     // swap(v, v): first = halves {lo,lo}, second = halves {hi,hi}
     const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return (l & 32) ? r[0] : r[1];
+    return lanes_in(0xFFFFFFFF00000000ull) ? r[0] : r[1];  // lanes with bit 32 set
   }
 }
 template <int J>
@@ -759,12 +694,23 @@ __device__ __forceinline__ uint64_t reverse_lanes64(uint64_t v) {
 // One compare-exchange step of the network: blocks of size K sorted in
 // alternating directions (all in the final direction at K = 64), partners J
 // lanes apart; ASC = ascending final order (lower lane keeps the smaller key).
+// Lanes that keep the larger key of their pair in step (K, J).
+constexpr uint64_t keep_max_lanes(int K, int J, bool ASC) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((((l & J) == 0) == ((K >= 64) || ((l & K) == 0))) != ASC) m |= 1ull << l;
+  return m;
+}
+// x stays where (x > partner) agrees with the lane's direction: the compare's
+// lane mask XOR the constant mask of the keep-min lanes (one scalar XOR).
+template <int K, int J, bool ASC>
+__device__ __forceinline__ uint64_t cex(uint64_t x, uint64_t y) {
+  constexpr uint64_t kmin = ~keep_max_lanes(K, J, ASC);
+  return lanes_in(__builtin_amdgcn_ballot_w64(x > y) ^ kmin) ? x : y;
+}
 template <int K, int J, bool ASC = false>
 __device__ __forceinline__ uint64_t bitonic_step(uint64_t x) {
-  const uint64_t y = xor_lane64<J>(x);
-  const int l = lane_id();
-  const bool keep_max = (((l & J) == 0) == ((K >= 64) || ((l & K) == 0))) != ASC;
-  return (keep_max == (x > y)) ? x : y;
+  return cex<K, J, ASC>(x, xor_lane64<J>(x));
 }
 template <bool ASC = false>
 __device__ __forceinline__ uint64_t wave_sort(uint64_t x) {
@@ -801,10 +747,8 @@ template <int K, int J>
 __device__ __forceinline__ void bitonic_step2(uint64_t &x, uint64_t &y) {
   const uint64_t xo = xor_lane64<J>(x);
   const uint64_t yo = xor_lane64<J>(y);
-  const int l = lane_id();
-  const bool keep_max = ((l & J) == 0) == ((K >= 64) || ((l & K) == 0));
-  x = (keep_max == (x > xo)) ? x : xo;
-  y = (keep_max != (y > yo)) ? y : yo;
+  x = cex<K, J, false>(x, xo);
+  y = cex<K, J, true>(y, yo);
 }
 __device__ __forceinline__ void wave_sort2(uint64_t &x, uint64_t &y) {
   bitonic_step2<2, 1>(x, y);
@@ -844,7 +788,6 @@ __device__ __forceinline__ bool topk_merge_general(const CallParams &p, const fl
                                                    const Cand *__restrict__ cand_row, TopkSmem &sm,
                                                    uint64_t (&kk)[kMergeSpec], bool reload) {
   const int V = p.vocab, K = p.top_k;
-  const bool pen = p.fuse_penalty != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslots = S * kCandCap;
   const int last_sh = last_region_sh(V, S);
@@ -852,7 +795,7 @@ __device__ __forceinline__ bool topk_merge_general(const CallParams &p, const fl
   __syncthreads();
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
   for (int base = 0; base < nslots; base += kMergeSpec * kBlock) {
-    if (base > 0 || reload || pen) {  // with the penalty: unpenalised keys, fresh
+    if (base > 0 || reload) {
 #pragma unroll
       for (int r = 0; r < kMergeSpec; ++r) {
         const int i = base + tid + r * kBlock;
@@ -865,7 +808,6 @@ __device__ __forceinline__ bool topk_merge_general(const CallParams &p, const fl
       const int i = base + tid + r * kBlock;
       vm |= (i < nslots && slot_valid(i, S, last_sh, sm)) ? (1u << r) : 0u;
     }
-    if (pen) pen_fix_keys(p, sm, kk, vm);
 #pragma unroll
     for (int r = 0; r < kMergeSpec; ++r) {
       if ((vm >> r) & 1u) {
@@ -1013,12 +955,9 @@ static_assert(kFastChunks / kWaves * 2 <= 8 && kWaves * kWaveCand + 128 <= kMerg
                   kWaveCand >= 128,
               "fast merge buffers");
 
-__device__ __forceinline__ int topk_merge_waves(const CallParams &p, const PenaltyPrefetch &pf,
-                                                const float (&gx)[kPenPerThread], int S,
-                                                const ChunkMeta *__restrict__ cm,
+__device__ __forceinline__ int topk_merge_waves(const CallParams &p, int S, const ChunkMeta *__restrict__ cm,
                                                 const Cand *__restrict__ cand_row, TopkSmem &sm) {
   const int V = p.vocab, K = p.top_k;
-  const bool pen = p.fuse_penalty != 0;
   const int lane = lane_id(), wv = threadIdx.x >> 6;
   // one round trip: the records (lane c < S) and this wave's candidate slots
   const int lc = min(lane, S - 1);
@@ -1061,12 +1000,8 @@ __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const Penal
       }
     }
   }
-  if (pen && wv == 0) {  // wave 1 writes wave 0's penalised logits back
-    sm.pid[lane] = pen_valid(p, pf, 0) ? pf.id[0] : -1;
-    sm.pgx[lane] = gx[0];
-  }
   uint64_t *wl = sm.buf.sk + wv * kWaveCand;
-  uint32_t nw = 0u, vmax_k = 0u;
+  uint32_t nw = 0u;
 #pragma unroll
   for (int j = 0; j < kFastChunks / kWaves; ++j) {
     if (wv + kWaves * j >= S) break;  // uniform
@@ -1076,76 +1011,47 @@ __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const Penal
       const uint64_t b = __ballot(ok);
       const uint32_t q = nw + lane_rank(b);
       if (ok && q < (uint32_t)kWaveCand) wl[q] = kk[2 * j + e];
-      if (ok) vmax_k = max(vmax_k, (uint32_t)(kk[2 * j + e] >> 32));
       nw += (uint32_t)__popcll(b);
     }
   }
-  // With the penalty, each lane penalises the list entries it owns (a key
-  // whose index is a history id); an entry that falls below T is cleared (it
-  // cannot be in the top K: at least K keys stay >= T, or the general merge
-  // runs) and no longer counted.
-  uint32_t live = nw;
-  if (pen) {
-    const double ip = 1.0 / (double)p.penalty;
-    const uint32_t nl = min(nw, (uint32_t)kWaveCand);
-    live = 0u;
-    vmax_k = 0u;
-    for (uint32_t i = (uint32_t)lane; i < nl; i += 64u) {
-      uint64_t k = wl[i];
-      const uint32_t c = pen_count(sm, ~(uint32_t)k);
-      if (c) {
-        k = ((uint64_t)ord_key(penalise_fast(key_float((uint32_t)(k >> 32)), (int)c, p.penalty, ip)) << 32) |
-            (uint32_t)k;
-        if (k < thr) k = 0ull;
-        wl[i] = k;
-      }
-      if (k >= thr) {
-        ++live;
-        vmax_k = max(vmax_k, (uint32_t)(k >> 32));
-      }
-    }
-    live = wave_sum_u32(live);
-  }
-  // Wave 0 alone from here: one radix digit (the highest bits in which T and
-  // the largest key differ; the bits above are common to every key >= T)
-  // narrows the nf keys to the m that can be in the top K: every key in bins
-  // above the bin holding the K-th key, and that bin.  With m <= 128 they are
-  // sorted as two interleaved 64-key networks and one merge.
-  vmax_k = wave_max_u32(vmax_k);
+  // The wave's list back in registers, entry lane and 64 + lane (the same
+  // wave wrote it: LDS order suffices).  With the penalty, a key whose index
+  // is a history id gets its penalised value; one that falls below T is no
+  // longer live (it cannot be in the top K: at least K keys stay >= T, or the
+  // general merge runs).
+  const uint32_t nl = min(nw, 128u);
+  const uint64_t e0 = ((uint32_t)lane < nl) ? wl[lane] : 0ull;
+  const uint64_t e1 = (64u + (uint32_t)lane < nl) ? wl[64 + lane] : 0ull;
+  const bool live0 = (uint32_t)lane < nl && e0 >= thr;
+  const bool live1 = 64u + (uint32_t)lane < nl && e1 >= thr;
+  const uint32_t vmax_k = wave_max_u32(max(live0 ? (uint32_t)(e0 >> 32) : 0u, live1 ? (uint32_t)(e1 >> 32) : 0u));
+  const uint32_t live = (uint32_t)__popcll(__ballot(live0)) + (uint32_t)__popcll(__ballot(live1));
   if (lane == 0) {
     sm.cnt[0][wv] = nw;
     sm.cnt[1][wv] = vmax_k;
     sm.cnt[2][wv] = live;
   }
   sm.hist[threadIdx.x] = 0u;  // kBlock == 256 bins
+  if (threadIdx.x == 0) sm.n = 0u;
   __syncthreads();
-  if (wv != 0) return 2;  // waves 1..3 wait at the final barrier of the caller
-  uint32_t nf = 0u, kmax = 0u, nwl[kWaves];
+  // Every wave from here (same values, same branches): one radix digit (the
+  // highest bits in which T and the largest key differ; the bits above are
+  // common to every key >= T) narrows the nf keys to the m that can be in the
+  // top K: every key in bins above the bin holding the K-th key, and that bin.
+  uint32_t nf = 0u, kmax = 0u;
   bool big = false;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    nwl[w] = sm.cnt[0][w];
     nf += sm.cnt[2][w];
     kmax = max(kmax, sm.cnt[1][w]);
-    big = big || nwl[w] > 128u;
+    big = big || sm.cnt[0][w] > 128u;
   }
-  if (big || nf < (uint32_t)K || kmax == T) return -2;
+  if (big || nf < (uint32_t)K || kmax == T) return -1;
   const int shift = (31 - __clz((int)(T ^ kmax))) & ~7;
-  // the four lists in registers (entry 64j + lane of list w), all read at
-  // once; bit 2w+j of vm: a live key (entries cleared by the penalty are not)
-  uint64_t kv[kWaves][2];
-  uint32_t vm = 0u;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t i = 64u * (uint32_t)j + (uint32_t)lane;
-      kv[w][j] = sm.buf.sk[w * kWaveCand + i];
-      vm |= (i < nwl[w] && kv[w][j] >= thr) ? (1u << (2 * w + j)) : 0u;
-    }
-#pragma unroll
-  for (int s = 0; s < 2 * kWaves; ++s)
-    if ((vm >> s) & 1u) atomicAdd(&sm.hist[(uint32_t)(kv[s >> 1][s & 1] >> (32 + shift)) & 255u], 1u);
+  const uint32_t d0 = (uint32_t)(e0 >> (32 + shift)) & 255u, d1 = (uint32_t)(e1 >> (32 + shift)) & 255u;
+  if (live0) atomicAdd(&sm.hist[d0], 1u);
+  if (live1) atomicAdd(&sm.hist[d1], 1u);
+  __syncthreads();
   // bins from the top: lane l holds bins 255-4l .. 252-4l
   const int b0 = 255 - 4 * lane;
   const uint32_t h0 = sm.hist[b0], h1 = sm.hist[b0 - 1], h2 = sm.hist[b0 - 2], h3 = sm.hist[b0 - 3];
@@ -1156,33 +1062,44 @@ __device__ __forceinline__ int topk_merge_waves(const CallParams &p, const Penal
   const int ls = __ffsll((unsigned long long)reach) - 1;  // reach != 0: nf >= K
   uint32_t bstar = 0u, m = 0u;
   {
-    const uint32_t e0 = readlane32(excl, ls);
+    const uint32_t e0s = readlane32(excl, ls);
     const uint32_t g0 = readlane32(h0, ls), g1 = readlane32(h1, ls), g2 = readlane32(h2, ls),
                    g3 = readlane32(h3, ls);
     const uint32_t bb = 255u - 4u * (uint32_t)ls;
-    if (e0 + g0 >= (uint32_t)K) { bstar = bb; m = e0 + g0; }
-    else if (e0 + g0 + g1 >= (uint32_t)K) { bstar = bb - 1u; m = e0 + g0 + g1; }
-    else if (e0 + g0 + g1 + g2 >= (uint32_t)K) { bstar = bb - 2u; m = e0 + g0 + g1 + g2; }
-    else { bstar = bb - 3u; m = e0 + g0 + g1 + g2 + g3; }
+    if (e0s + g0 >= (uint32_t)K) { bstar = bb; m = e0s + g0; }
+    else if (e0s + g0 + g1 >= (uint32_t)K) { bstar = bb - 1u; m = e0s + g0 + g1; }
+    else if (e0s + g0 + g1 + g2 >= (uint32_t)K) { bstar = bb - 2u; m = e0s + g0 + g1 + g2; }
+    else { bstar = bb - 3u; m = e0s + g0 + g1 + g2 + g3; }
   }
-  if (m > 128u) return -2;
-  // the m keys with digit >= bstar, and the largest value key below them
+  if (m > 128u) return -1;
+  // each wave's keys with digit >= bstar go to sel (offset by an LDS counter);
+  // the largest value key below them is kept per wave
   uint64_t *sel = sm.buf.sk + kWaves * kWaveCand;
-  uint32_t ns = 0u, below = 0u;
-#pragma unroll
-  for (int s = 0; s < 2 * kWaves; ++s) {
-    const uint64_t k = kv[s >> 1][s & 1];
-    const bool v = (vm >> s) & 1u;
-    const bool in = v && (((uint32_t)(k >> (32 + shift)) & 255u) >= bstar);
-    const uint64_t bm = __ballot(in);
-    if (in) sel[ns + lane_rank(bm)] = k;
-    else if (v) below = max(below, (uint32_t)(k >> 32));
-    ns += (uint32_t)__popcll(bm);
+  const bool in0 = live0 && d0 >= bstar, in1 = live1 && d1 >= bstar;
+  const uint64_t bm0 = __ballot(in0), bm1 = __ballot(in1);
+  const uint32_t cw0 = (uint32_t)__popcll(bm0);
+  uint32_t off = 0u;
+  if (lane == 0) off = atomicAdd(&sm.n, cw0 + (uint32_t)__popcll(bm1));
+  off = readlane32(off, 0);
+  if (in0) sel[off + lane_rank(bm0)] = e0;
+  if (in1) sel[off + cw0 + lane_rank(bm1)] = e1;
+  const uint32_t bw = wave_max_u32(max((live0 && !in0) ? (uint32_t)(e0 >> 32) : 0u,
+                                       (live1 && !in1) ? (uint32_t)(e1 >> 32) : 0u));
+  if (lane == 0) sm.cnt[3][wv] = bw;
+  __syncthreads();
+  // wave 0 sorts sel[0, 64) descending, wave 1 sorts sel[64, 128) ascending
+  // (back into place)
+  uint64_t x = 0ull;
+  if (wv == 0) {
+    x = wave_sort<false>(((uint32_t)lane < m) ? sel[lane] : 0ull);
+  } else if (wv == 1) {
+    const uint64_t y = wave_sort<true>((64u + (uint32_t)lane < m) ? sel[64 + lane] : 0ull);
+    sel[64 + lane] = y;
   }
-  below = wave_max_u32(below);
-  uint64_t x = ((uint32_t)lane < m) ? sel[lane] : 0ull;
-  uint64_t y = (64u + (uint32_t)lane < m) ? sel[64 + lane] : 0ull;
-  wave_sort2(x, y);  // x descending, y ascending
+  __syncthreads();
+  if (wv != 0) return 2;  // waves 1..3 wait at the final barrier of the caller
+  const uint32_t below = max(max(sm.cnt[3][0], sm.cnt[3][1]), max(sm.cnt[3][2], sm.cnt[3][3]));
+  const uint64_t y = sel[64 + lane];
   const uint64_t lo = x > y ? y : x;
   x = wave_merge<false>(x > y ? x : y);
   // The reference keeps the top K; if the K-th value is shared by a stored
@@ -1214,7 +1131,6 @@ __device__ __forceinline__ bool topk_merge(const CallParams &p, const float *__r
                                            const ChunkMeta *__restrict__ cm,
                                            const Cand *__restrict__ cand_row, TopkSmem &sm) {
   const int V = p.vocab, K = p.top_k;
-  const bool pen = p.fuse_penalty != 0;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslots = S * kCandCap;
   uint32_t fl = 0u, tmx = 0u;
@@ -1268,12 +1184,6 @@ __device__ __forceinline__ bool topk_merge(const CallParams &p, const float *__r
       const int i = base + tid + r * kBlock;
       vb |= (i < nslots && kk[r] >= thr && slot_valid(i, S, last_sh, sm)) ? (1u << r) : 0u;
     }
-    if (pen) {  // penalised keys (this batch only: fresh loads each round)
-      pen_fix_keys(p, sm, kk, vb);
-#pragma unroll
-      for (int r = 0; r < kMergeSpec; ++r)
-        if (kk[r] < thr) vb &= ~(1u << r);
-    }
     m = (uint32_t)__popc(vb);
     const uint32_t incl = wave_incl_scan_u32(m);
     if (lane == 63) sm.wtot[wv] = incl;
@@ -1295,7 +1205,7 @@ __device__ __forceinline__ bool topk_merge(const CallParams &p, const float *__r
     __syncthreads();
   }
   if (nf < (uint32_t)K || nf > (uint32_t)kMergeTop)
-    return topk_merge_general<VEC>(p, L, S, cand_row, sm, kk, pen || nslots > kMergeSpec * kBlock);
+    return topk_merge_general<VEC>(p, L, S, cand_row, sm, kk, nslots > kMergeSpec * kBlock);
 
   // top 64 of the nf <= 512 keys
   uint64_t *R = sm.buf.sk + kMergeTop;  // four sorted lists of 64
@@ -1726,57 +1636,32 @@ __device__ __forceinline__ void topk_body(const CallParams &p) {
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
   RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
-  const bool pen = p.fuse_penalty != 0;
   PenaltyPrefetch pf;
-  if (pen) {
+  if (p.fuse_penalty) {
     penalty_prefetch(p, row, pf);  // issued before the chunk
-    penalty_table_clear(sm);       // the stream phase's barriers order it before the inserts
+    penalty_clear(sm);             // ordered before the table by the stream phase's barrier
   }
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
-                        cm + chunk, sm);
-  // with the penalty, every workgroup counts the history ids while its ticket
-  // is in flight (the winner needs the table; the others are done anyway)
-  if (!last_of_row(p.tickets, row, S, &sm.last, [&] {
-        if (pen) penalty_table(p, pf, sm);
-      }))
-    return;
-  float gx[kPenPerThread];
-  if (pen) {  // the logits at the history ids, gathered before the merge's loads
-#pragma unroll
-    for (int r = 0; r < kPenPerThread; ++r) gx[r] = pen_valid(p, pf, r) ? xloadf(&L[pf.id[r]]) : 0.0f;
-  }
+                        cm + chunk, pf, sm);
+  if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
   if (threadIdx.x == 0) {
     sm.uval = rng_draw(p.rng, row, rp);
     sm.replay = 1;
   }
   __syncthreads();
   int mr = -1;
-  bool written = false;  // penalised logits stored (not yet known to be visible)
   if (S <= kFastChunks) {
-    // wave 0 finishes the fast merge alone while waves 1-3 write the
-    // penalised logits back; the verdict is shared at the barrier
-    const int r = topk_merge_waves(p, pf, gx, S, cm, cr, sm);
-    if (r == 2 && pen) penalty_write_back(p, row, pf, gx, sm, true);
+    // waves 0-3 narrow the candidates, waves 0 and 1 sort; the verdict is
+    // shared at the barrier
+    const int r = topk_merge_waves(p, S, cm, cr, sm);
     if (threadIdx.x == 0) sm.mres = r;
     __syncthreads();
     const int m0 = sm.mres;
-    written = (m0 == 1 || m0 == -2);
     mr = (m0 == 1) ? ((sm.ntop == K) ? 1 : 0) : (m0 == 0 ? 0 : -1);
-  }
-  if (pen && (!written || mr < 0)) {  // the general merge re-reads the row: stores visible
-    if (!written) penalty_write_back(p, row, pf, gx, sm, false);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
   }
   if (mr < 0) mr = topk_merge<VEC>(p, L, S, cm, cr, sm) ? 1 : 0;
   if (mr > 0) topk_fast(p, row, sm);
-  if (sm.replay) {
-    if (p.fuse_penalty) {  // the replay re-reads the row: the stores must be visible
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    topk_replay(p, row, sm);
-  }
+  if (sm.replay) topk_replay(p, row, sm);
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
