@@ -122,6 +122,40 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
                     int32_t vocab, float *logits, int64_t logit_stride, float *scratch,
                     void *stream);
 
+/* lm_head weight formats: the GGML tensor type ids (GGUFReader.pas:34-42)
+ * that TVdxAttention.DispatchMatVec selects a shader by (Attention.pas:994-1014). */
+#define VDX_TENSOR_F16 1   /* in_dim fp16 values per row (matvec_f16.comp)          */
+#define VDX_TENSOR_Q4_0 2  /* 18-byte blocks: fp16 d, 16 bytes of nibbles          */
+#define VDX_TENSOR_Q8_0 8  /* 34-byte blocks: fp16 d, 32 int8 (matvec_q8_0.comp)   */
+
+/* TVdxModel.UnembedToLogits (Model.pas:1258-1270) batched over `rows` hidden
+ * vectors: the output RMSNorm as TVdxLayerNorm.ApplyCopy issues it
+ * (LayerNorm.pas:395-417, shaders/rmsnorm_copy.comp:
+ *   xn[e] = (h[e] * inv_rms) * norm_weight[e],
+ *   inv_rms = 1 / sqrt(sum_e h[e]^2 / in_dim + norm_eps)),
+ * skipped when `norm_weight` is NULL, then the lm_head in the weight tensor's
+ * own format `wtype` (VDX_TENSOR_*), as TVdxAttention.DispatchMatVec issues it
+ * (Attention.pas:979-1025): logits[r*logit_stride + v] = sum_e W(v,e) * xn_r[e].
+ * `weights` is 16-byte aligned; in_dim is a multiple of 256; `scratch` (at
+ * least 16*in_dim floats) holds the prepared hidden rows and is required when
+ * rows > 1 or with the norm.  Every pointer is device memory.  Stream-ordered,
+ * asynchronous, allocates nothing; a failure's message is
+ * vdx_sampler_last_error(NULL); an unknown wtype is VDX_E_UNSUPPORTED. */
+int vdx_lmhead(const void *weights, int32_t wtype, const float *hidden, const float *norm_weight,
+               float norm_eps, int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
+               int64_t logit_stride, float *scratch, void *stream);
+
+/* RunUnembedding followed by Process (Inference.pas:327-339) with the logits
+ * kept in HBM: UnembedToLogits (as vdx_lmhead, the sampler's own workspace as
+ * scratch) writes rows x vocab logits into `logits` (device, row stride
+ * logit_stride >= vocab) or, when `logits` is NULL, into the sampler's own
+ * workspace (allocated on the first call with a larger rows*vocab); the rows
+ * are then sampled exactly as by vdx_sampler_process_device. */
+int vdx_sampler_lmhead_device(vdx_sampler *s, const void *weights, int32_t wtype, const float *hidden,
+                              const float *norm_weight, float norm_eps, int32_t rows, int32_t in_dim,
+                              int32_t vocab, float *logits, int64_t logit_stride,
+                              const float *uniforms, const vdx_sample_outputs *out, void *stream);
+
 /* RunUnembedding followed by Process (Inference.pas:327-339) with the logits
  * kept in HBM: the Q4_0 lm_head (as vdx_lmhead_q4_0) writes rows x vocab
  * logits into `logits` (device, row stride logit_stride >= vocab) or, when

@@ -606,27 +606,156 @@ void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
   }
 }
 
+/* matvec_q8_0.comp:53-93: block layout :5-9 (34 bytes: f16 d, 32 int8);
+ * 256 lanes, lane t sums elements t, t+256, ... as acc += (q * d) * x
+ * (:74-78), then the LDS tree (:83-89). */
+void vdxo_matvec_q8_0(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                      float *logits) {
+  const int32_t bpr = in_dim >> 5;
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint8_t *row = w + (int64_t)r * bpr * 34;
+    float partial[256];
+    for (int32_t tid = 0; tid < 256; ++tid) {
+      float acc = 0.0f;
+      for (int32_t e = tid; e < in_dim; e += 256) {
+        const uint8_t *b = row + (int64_t)(e >> 5) * 34;
+        const float d = vdxo_half_to_float((uint16_t)(b[0] | (b[1] << 8)));
+        const float q = (float)(int8_t)b[2 + (e & 31)];
+        float t = q * d;
+        t = t * x[e];
+        acc = acc + t;
+      }
+      partial[tid] = acc;
+    }
+    for (int32_t stride = 128; stride > 0; stride >>= 1)
+      for (int32_t tid = 0; tid < stride; ++tid) partial[tid] = partial[tid] + partial[tid + stride];
+    logits[r] = partial[0];
+  }
+}
+
+/* The library kernel's order for Q8_0: per block k, s = fmaf(q_i, x, s) for
+ * i = 0..31, acc = fmaf(d_k, s, acc). */
+void vdxo_matvec_q8_0_blocked(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                              float *logits) {
+  const int32_t bpr = in_dim >> 5;
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint8_t *row = w + (int64_t)r * bpr * 34;
+    float acc = 0.0f;
+    for (int32_t k = 0; k < bpr; ++k) {
+      const uint8_t *b = row + (int64_t)k * 34;
+      const float d = vdxo_half_to_float((uint16_t)(b[0] | (b[1] << 8)));
+      float s = 0.0f;
+      for (int32_t i = 0; i < 32; ++i) s = fmaf((float)(int8_t)b[2 + i], x[32 * k + i], s);
+      acc = fmaf(d, s, acc);
+    }
+    logits[r] = acc;
+  }
+}
+
+/* matvec_f16.comp:43-80: packed f16 pairs, 256 lanes, lane t takes pairs
+ * t, t+256, ... as acc += w.x * x[2d]; acc += w.y * x[2d+1] (:56-63), then
+ * the LDS tree (:68-74). */
+void vdxo_matvec_f16(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                     float *logits) {
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint8_t *row = w + (int64_t)r * in_dim * 2;
+    float partial[256];
+    for (int32_t tid = 0; tid < 256; ++tid) {
+      float acc = 0.0f;
+      for (int32_t d = tid; d < in_dim / 2; d += 256) {
+        const uint8_t *p = row + 4 * (int64_t)d;
+        const float w0 = vdxo_half_to_float((uint16_t)(p[0] | (p[1] << 8)));
+        const float w1 = vdxo_half_to_float((uint16_t)(p[2] | (p[3] << 8)));
+        float t = w0 * x[2 * d];
+        acc = acc + t;
+        t = w1 * x[2 * d + 1];
+        acc = acc + t;
+      }
+      partial[tid] = acc;
+    }
+    for (int32_t stride = 128; stride > 0; stride >>= 1)
+      for (int32_t tid = 0; tid < stride; ++tid) partial[tid] = partial[tid] + partial[tid + stride];
+    logits[r] = partial[0];
+  }
+}
+
+/* The library kernel's order for F16: per 32-element block k, s = fmaf(w_i,
+ * x, s) for i = 0..31, acc = acc + s. */
+void vdxo_matvec_f16_blocked(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                             float *logits) {
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint8_t *row = w + (int64_t)r * in_dim * 2;
+    float acc = 0.0f;
+    for (int32_t k = 0; k < in_dim / 32; ++k) {
+      float s = 0.0f;
+      for (int32_t i = 0; i < 32; ++i) {
+        const uint8_t *p = row + 2 * (int64_t)(32 * k + i);
+        s = fmaf(vdxo_half_to_float((uint16_t)(p[0] | (p[1] << 8))), x[32 * k + i], s);
+      }
+      acc = acc + s;
+    }
+    logits[r] = acc;
+  }
+}
+
+/* rmsnorm_copy.comp:40-74 (TVdxLayerNorm.ApplyCopy, LayerNorm.pas:395-417):
+ * 256 lanes sum source[i]^2 strided (:45-50), the LDS tree (:55-60),
+ * inv_rms = 1 / sqrt(ss / dim + eps) (:63-65), dest[i] = (source[i] *
+ * inv_rms) * weight[i] (:70-73); IEEE division and square root. */
+void vdxo_rmsnorm(const float *h, const float *wt, float eps, int32_t dim, float *out) {
+  float part[256];
+  for (int32_t t = 0; t < 256; ++t) {
+    float ss = 0.0f;
+    for (int32_t i = t; i < dim; i += 256) {
+      const float sq = h[i] * h[i];
+      ss = ss + sq;
+    }
+    part[t] = ss;
+  }
+  for (int32_t stride = 128; stride > 0; stride >>= 1)
+    for (int32_t t = 0; t < stride; ++t) part[t] = part[t] + part[t + stride];
+  const float inv = 1.0f / sqrtf(part[0] / (float)dim + eps);
+  for (int32_t i = 0; i < dim; ++i) {
+    const float a = h[i] * inv;
+    out[i] = a * wt[i];
+  }
+}
+
+typedef void (*mv_fn)(const uint8_t *, const float *, int32_t, int32_t, float *);
+
+static int64_t mv_row_bytes(int32_t wtype, int32_t in_dim) {
+  return wtype == 2 ? (int64_t)(in_dim >> 5) * 18 : wtype == 8 ? (int64_t)(in_dim >> 5) * 34
+                                                               : (int64_t)in_dim * 2;
+}
+
+static mv_fn mv_pick(int32_t wtype, int32_t blocked) {
+  if (wtype == 2) return blocked ? vdxo_matvec_q4_0_blocked : vdxo_matvec_q4_0;
+  if (wtype == 8) return blocked ? vdxo_matvec_q8_0_blocked : vdxo_matvec_q8_0;
+  return blocked ? vdxo_matvec_f16_blocked : vdxo_matvec_f16;
+}
+
 typedef struct {
   const uint8_t *w;
   const float *x;
-  int32_t in_dim, r0, r1, blocked;
+  int32_t in_dim, r0, r1, blocked, wtype;
   float *out;
 } mv_job;
 
 static void *mv_worker(void *arg) {
   const mv_job *j = (const mv_job *)arg;
-  const int64_t rb = (int64_t)(j->in_dim >> 5) * 18;
-  if (j->r1 > j->r0) {
-    if (j->blocked)
-      vdxo_matvec_q4_0_blocked(j->w + rb * j->r0, j->x, j->in_dim, j->r1 - j->r0, j->out + j->r0);
-    else
-      vdxo_matvec_q4_0(j->w + rb * j->r0, j->x, j->in_dim, j->r1 - j->r0, j->out + j->r0);
-  }
+  const int64_t rb = mv_row_bytes(j->wtype, j->in_dim);
+  if (j->r1 > j->r0)
+    mv_pick(j->wtype, j->blocked)(j->w + rb * j->r0, j->x, j->in_dim, j->r1 - j->r0, j->out + j->r0);
   return NULL;
 }
 
 void vdxo_matvec_q4_0_mt(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
                          float *logits, int32_t blocked, int32_t threads) {
+  vdxo_matvec_mt(w, 2, x, in_dim, rows, logits, blocked, threads);
+}
+
+void vdxo_matvec_mt(const uint8_t *w, int32_t wtype, const float *x, int32_t in_dim, int32_t rows,
+                    float *logits, int32_t blocked, int32_t threads) {
   if (threads < 1) threads = 1;
   pthread_t *tid = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
   mv_job *jobs = (mv_job *)malloc(sizeof(mv_job) * (size_t)threads);
@@ -638,6 +767,7 @@ void vdxo_matvec_q4_0_mt(const uint8_t *w, const float *x, int32_t in_dim, int32
     j->r0 = (int32_t)((int64_t)rows * t / threads);
     j->r1 = (int32_t)((int64_t)rows * (t + 1) / threads);
     j->blocked = blocked;
+    j->wtype = wtype;
     j->out = logits;
     pthread_create(&tid[t], NULL, mv_worker, j);
   }

@@ -144,6 +144,25 @@ void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
  * rows split evenly. */
 void vdxo_matvec_q4_0_mt(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
                          float *logits, int32_t blocked, int32_t threads);
+/* ---- Q8_0 / F16 lm_head and the output RMSNorm ---------------------------- */
+/* shaders/matvec_q8_0.comp: 256 strided lanes, acc += (q * d) * x, LDS tree. */
+void vdxo_matvec_q8_0(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                      float *logits);
+/* The library kernel's Q8_0 order: per block s = fmaf(q_i, x, s), acc = fmaf(d, s, acc). */
+void vdxo_matvec_q8_0_blocked(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                              float *logits);
+/* shaders/matvec_f16.comp: 256 strided lanes over f16 pairs, LDS tree. */
+void vdxo_matvec_f16(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                     float *logits);
+/* The library kernel's F16 order: per 32 elements s = fmaf(w_i, x, s), acc = acc + s. */
+void vdxo_matvec_f16_blocked(const uint8_t *w, const float *x, int32_t in_dim, int32_t rows,
+                             float *logits);
+/* Any of the three formats (wtype: GGML id 1 F16, 2 Q4_0, 8 Q8_0), either
+ * order, over `threads` POSIX threads. */
+void vdxo_matvec_mt(const uint8_t *w, int32_t wtype, const float *x, int32_t in_dim, int32_t rows,
+                    float *logits, int32_t blocked, int32_t threads);
+/* shaders/rmsnorm_copy.comp (TVdxLayerNorm.ApplyCopy). */
+void vdxo_rmsnorm(const float *h, const float *w, float eps, int32_t dim, float *out);
 /* fp16 -> fp32 (IEEE binary16), as unpackHalf2x16. */
 float vdxo_half_to_float(uint16_t h);
 

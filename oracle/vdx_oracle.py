@@ -112,6 +112,12 @@ def lib():
                                                P(C.c_float)]
         L.vdxo_matvec_q4_0_mt.argtypes = [P(C.c_uint8), P(C.c_float), C.c_int32, C.c_int32,
                                           P(C.c_float), C.c_int32, C.c_int32]
+        for fn in ("vdxo_matvec_q8_0", "vdxo_matvec_q8_0_blocked", "vdxo_matvec_f16",
+                   "vdxo_matvec_f16_blocked"):
+            getattr(L, fn).argtypes = [P(C.c_uint8), P(C.c_float), C.c_int32, C.c_int32, P(C.c_float)]
+        L.vdxo_matvec_mt.argtypes = [P(C.c_uint8), C.c_int32, P(C.c_float), C.c_int32, C.c_int32,
+                                     P(C.c_float), C.c_int32, C.c_int32]
+        L.vdxo_rmsnorm.argtypes = [P(C.c_float), P(C.c_float), C.c_float, C.c_int32, P(C.c_float)]
         L.vdxo_half_to_float.argtypes = [C.c_uint16]
         L.vdxo_half_to_float.restype = C.c_float
         _lib = L
@@ -230,6 +236,37 @@ def matvec_q4_0_mt(w: np.ndarray, x: np.ndarray, in_dim: int, rows: int, blocked
     x = np.ascontiguousarray(x, dtype=np.float32)
     lib().vdxo_matvec_q4_0_mt(w.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(x), in_dim, rows,
                               _fp(out), 1 if blocked else 0, int(threads))
+    return out
+
+
+TENSOR_F16, TENSOR_Q4_0, TENSOR_Q8_0 = 1, 2, 8  # GGML type ids (GGUFReader.pas:34-42)
+_MV = {(TENSOR_Q4_0, False): "vdxo_matvec_q4_0", (TENSOR_Q4_0, True): "vdxo_matvec_q4_0_blocked",
+       (TENSOR_Q8_0, False): "vdxo_matvec_q8_0", (TENSOR_Q8_0, True): "vdxo_matvec_q8_0_blocked",
+       (TENSOR_F16, False): "vdxo_matvec_f16", (TENSOR_F16, True): "vdxo_matvec_f16_blocked"}
+
+
+def matvec(w: np.ndarray, wtype: int, x: np.ndarray, in_dim: int, rows: int, blocked: bool,
+           threads: int = 1) -> np.ndarray:
+    """The lm_head of one hidden vector in the shader's order (blocked=False)
+    or the library kernel's (blocked=True), for wtype TENSOR_Q4_0 / _Q8_0 / _F16."""
+    out = np.zeros(rows, dtype=np.float32)
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if threads > 1:
+        lib().vdxo_matvec_mt(w.ctypes.data_as(C.POINTER(C.c_uint8)), int(wtype), _fp(x), in_dim, rows,
+                             _fp(out), 1 if blocked else 0, int(threads))
+    else:
+        getattr(lib(), _MV[(int(wtype), bool(blocked))])(w.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(x),
+                                                        in_dim, rows, _fp(out))
+    return out
+
+
+def rmsnorm(h: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """shaders/rmsnorm_copy.comp on one vector."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros_like(h)
+    lib().vdxo_rmsnorm(_fp(h), _fp(w), float(eps), int(h.size), _fp(out))
     return out
 
 

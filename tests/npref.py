@@ -156,6 +156,21 @@ def penalty(L, hist, p):
 
 
 # --- Q4_0 (shaders/matvec_q4_0.comp:7-15) --------------------------------
+def q8_0_dequant(w: np.ndarray, in_dim: int, rows: int) -> np.ndarray:
+    """Closed-form dequantisation of rows x in_dim Q8_0 (34-byte blocks: fp16
+    d, 32 int8)."""
+    nb = in_dim // 32
+    blk = w.reshape(rows, nb, 34)
+    d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    q = blk[:, :, 2:34].copy().view(np.int8).astype(np.float32)
+    return (q * d).reshape(rows, in_dim)
+
+
+def f16_dequant(w: np.ndarray, in_dim: int, rows: int) -> np.ndarray:
+    """rows x in_dim fp16 values, widened."""
+    return np.ascontiguousarray(w).view(np.float16).reshape(rows, in_dim).astype(np.float32)
+
+
 def q4_0_dequant(w: np.ndarray, in_dim: int, rows: int) -> np.ndarray:
     """Closed-form dequantisation of rows x in_dim Q4_0 (18-byte blocks)."""
     nb = in_dim // 32

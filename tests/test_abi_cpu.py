@@ -112,3 +112,11 @@ def test_lmhead_argument_errors_need_no_gpu():
         rc = L.vdx_lmhead_q4_0(w, h, rows, d, v, C.c_void_p(al), v, C.c_void_p(al), None)
         assert rc == -1
         assert msg in L.vdx_sampler_last_error(None).decode()
+    # the general entry point: an unknown weight type is unsupported; the norm
+    # needs the scratch copy even for one row
+    rc = L.vdx_lmhead(C.c_void_p(al), 0, hid, None, C.c_float(1e-6), 1, 256, 1024, C.c_void_p(al), 1024,
+                      C.c_void_p(al), None)
+    assert rc == -3 and "weight type" in L.vdx_sampler_last_error(None).decode()
+    rc = L.vdx_lmhead(C.c_void_p(al), 8, hid, hid, C.c_float(1e-6), 1, 256, 1024, C.c_void_p(al), 1024,
+                      None, None)
+    assert rc == -1 and "scratch" in L.vdx_sampler_last_error(None).decode()

@@ -191,3 +191,93 @@ def test_lmhead_greedy_and_penalty():
         pen = npref.penalty(raw, hist[b], 1.3)
         assert np.array_equal(Lp[b].view(np.uint32), pen.view(np.uint32))
         assert tok[b] == int(np.argmax(pen))
+
+
+# ---- Q8_0 / F16 lm_head and the fused output RMSNorm -----------------------------
+def rand_q8_0(rng, rows, in_dim):
+    nb = in_dim // 32
+    blk = rng.integers(0, 256, (rows, nb, 34), dtype=np.uint8)
+    d = np.abs(rng.standard_normal((rows, nb)) * 0.02).astype(np.float16)
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    return blk.reshape(-1)
+
+
+def rand_f16(rng, rows, in_dim):
+    return (rng.standard_normal((rows, in_dim)) * 0.05).astype(np.float16).view(np.uint8).reshape(-1)
+
+
+def gpu_lmhead_any(w, wtype, H, V, norm=None, eps=1e-6):
+    import torch
+
+    from vindexllm_amd import lmhead
+
+    dev = torch.device("cuda:0")
+    wd = torch.from_numpy(w).to(dev)
+    hd = torch.from_numpy(np.ascontiguousarray(H)).to(dev)
+    nd = torch.from_numpy(norm).to(dev) if norm is not None else None
+    out = lmhead(wd, wtype, hd, V, norm_weight=nd, norm_eps=eps)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("wtype", [O.TENSOR_Q8_0, O.TENSOR_F16, O.TENSOR_Q4_0])
+@pytest.mark.parametrize("V,D,B,norm", [(4096 + 77, 256, 1, False), (4096 + 77, 256, 3, True),
+                                        (2048, 512, 8, False), (1000, 2560, 16, True),
+                                        (1000, 2560, 1, True), (300, 256, 17, False)])
+def test_lmhead_formats_and_norm_bit_exact(wtype, V, D, B, norm):
+    # every format's logits equal the oracle's restatement of the kernel's
+    # summation order, on the output-RMSNorm'd rows when the norm is fused
+    log(f"[case] lm_head wtype={wtype} V={V} D={D} B={B} norm={norm}")
+    rng = np.random.default_rng(7000 + wtype * 100 + V + D + B)
+    w = {O.TENSOR_Q8_0: rand_q8_0, O.TENSOR_F16: rand_f16, O.TENSOR_Q4_0: rand_q4_0}[wtype](rng, V, D)
+    H = (rng.standard_normal((B, D)) * 4.0).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    G = gpu_lmhead_any(w, wtype, H, V, norm=nw)
+    for b in range(B):
+        xn = O.rmsnorm(H[b], nw, 1e-6) if norm else H[b]
+        want = O.matvec(w, wtype, xn, D, V, True)
+        assert np.array_equal(G[b].view(np.uint32), want.view(np.uint32)), \
+            f"row {b}: {np.flatnonzero(G[b] != want)[:5]}"
+    log(f"[done] lm_head wtype={wtype} V={V} D={D} B={B} norm={norm}")
+
+
+def test_lmhead_device_q8_0_norm_sampling():
+    # UnembedToLogits (norm + Q8_0 head) followed by the sampler, end to end,
+    # at Gemma-3-4B's shape with four hidden rows: logits bit-exact with the
+    # kernel-order restatement (the shader order's fp32 bound is pinned on the
+    # CPU), sampling at the sampler's bar
+    import torch
+
+    from vindexllm_amd import VDX_TENSOR_Q8_0, TVdxSampler
+
+    V, D, B = 262144, 2560, 4
+    rng = np.random.default_rng(4242)
+    w = rand_q8_0(rng, V, D)
+    H = (rng.standard_normal((B, D)) * 3.0).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    u = u_stream(np.random.default_rng(4243), B)
+    cfg = dict(temperature=1.0, top_k=64, top_p=0.95)
+    log("[case] Q8_0 + RMSNorm lm_head + top-k64/top-p0.95 B=4")
+    dev = torch.device("cuda:0")
+    wd, hd, nd = (torch.from_numpy(a).to(dev) for a in (w, H, nw))
+    L = torch.empty(B, V, dtype=torch.float32, device=dev)
+    ti = torch.full((B, 64), -1, dtype=torch.int32, device=dev)
+    tp = torch.full((B, 64), -1.0, dtype=torch.float32, device=dev)
+    fl = torch.zeros(B, dtype=torch.int32, device=dev)
+    with TVdxSampler(0, B) as s:
+        c = s.DefaultConfig()
+        c.Temperature, c.TopK, c.TopP = 1.0, 64, 0.95
+        s.SetConfig(c)
+        tok = s.lmhead_device(wd, VDX_TENSOR_Q8_0, hd, V, norm_weight=nd, logits=L,
+                              uniforms=torch.from_numpy(u).to(dev), topk_idx=ti, topk_prob=tp, flags=fl)
+        torch.cuda.synchronize()
+    Lg = L.cpu().numpy()
+    for b in range(B):
+        xn = O.rmsnorm(H[b], nw, 1e-6)
+        want = O.matvec(w, O.TENSOR_Q8_0, xn, D, V, True, threads=THREADS)
+        assert np.array_equal(Lg[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    g = dict(tokens=tok.cpu().numpy(), topk_idx=ti.cpu().numpy(), topk_prob=tp.cpu().numpy(),
+             flags=fl.cpu().numpy(), logits_after=Lg)
+    orc = oracle_rows(Lg, cfg, u)
+    compare(g, orc, cfg, check_logits=False, label="Q8_0+norm B=4")
+    log("[done] Q8_0 + RMSNorm lm_head + sampling")

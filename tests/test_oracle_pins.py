@@ -466,3 +466,104 @@ def test_q4_0_blocked_within_fp32_error_bound():
     assert (np.abs(shader - exact) <= (in_dim // 64 + 6 + 1) * u * mag).all()
     # the two orders agree far inside the bound on typical rows
     assert np.median(np.abs(blocked - shader) / mag) < 1e-7
+
+
+# ---- Q8_0 / F16 lm_head and the output RMSNorm (matvec_q8_0.comp,
+# ---- matvec_f16.comp, rmsnorm_copy.comp) ---------------------------------------
+def _rand_q8_0(rng, rows, in_dim, exact=False):
+    nb = in_dim // 32
+    blk = np.zeros((rows, nb, 34), dtype=np.uint8)
+    if exact:
+        d = np.where(rng.random((rows, nb)) < 0.5, 2.0 ** -4, 2.0 ** -3).astype(np.float16)
+    else:
+        d = np.abs(rng.standard_normal((rows, nb)) * 0.02).astype(np.float16)
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    blk[:, :, 2:] = rng.integers(0, 256, (rows, nb, 32), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def _rand_f16(rng, rows, in_dim, exact=False):
+    if exact:  # multiples of 1/8 in [-8, 8)
+        w = (rng.integers(-64, 64, (rows, in_dim)) / 8.0).astype(np.float16)
+    else:
+        w = (rng.standard_normal((rows, in_dim)) * 0.05).astype(np.float16)
+    return w.view(np.uint8).reshape(-1)
+
+
+@pytest.mark.parametrize("wtype", [O.TENSOR_Q8_0, O.TENSOR_F16])
+def test_q8_f16_both_orders_exact_on_exact_inputs(wtype):
+    # closed form: with power-of-two scales, weights and hidden values on a
+    # coarse grid every product and partial sum is exact, so both
+    # restatements equal the float64 dot product of the dequantised rows
+    rng = np.random.default_rng(31 + wtype)
+    for in_dim in (256, 2560):
+        rows = 24
+        if wtype == O.TENSOR_Q8_0:
+            w = _rand_q8_0(rng, rows, in_dim, exact=True)
+            W = npref.q8_0_dequant(w, in_dim, rows).astype(np.float64)
+            x = (rng.integers(-4, 4, in_dim) / 8.0).astype(np.float32)
+        else:
+            w = _rand_f16(rng, rows, in_dim, exact=True)
+            W = npref.f16_dequant(w, in_dim, rows).astype(np.float64)
+            x = (rng.integers(-8, 8, in_dim) / 8.0).astype(np.float32)
+        want = W @ x.astype(np.float64)
+        for blocked in (False, True):
+            assert np.array_equal(O.matvec(w, wtype, x, in_dim, rows, blocked).astype(np.float64), want)
+            assert np.array_equal(O.matvec(w, wtype, x, in_dim, rows, blocked, threads=3).astype(np.float64),
+                                  want)
+
+
+def test_q8_0_byte_order_is_pinned():
+    # one non-zero int8 at each element position in turn: only the documented
+    # layout (scale in bytes 0-1, element i in byte 2 + i, signed) reproduces
+    # x[e] * q * d at position e
+    in_dim = 256
+    x = (np.arange(in_dim) + 1).astype(np.float32)
+    for e in (0, 1, 31, 32, 33, 100, 255):
+        blk = np.zeros((in_dim // 32, 34), dtype=np.uint8)
+        blk[:, 0:2] = np.array([2.0], dtype=np.float16).view(np.uint8)
+        k, i = divmod(e, 32)
+        blk[k, 2 + i] = np.array([-3], dtype=np.int8).view(np.uint8)[0]
+        for blocked in (False, True):
+            got = O.matvec(blk.reshape(-1), O.TENSOR_Q8_0, x, in_dim, 1, blocked)[0]
+            assert got == np.float32(-6.0 * (e + 1))
+
+
+def test_q8_f16_within_fp32_error_bound():
+    rng = np.random.default_rng(33)
+    rows, in_dim = 128, 2560
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    u = 2.0 ** -24
+    for wtype, w, deq in ((O.TENSOR_Q8_0, _rand_q8_0(rng, rows, in_dim), npref.q8_0_dequant),
+                          (O.TENSOR_F16, _rand_f16(rng, rows, in_dim), npref.f16_dequant)):
+        W = deq(w, in_dim, rows).astype(np.float64)
+        exact = W @ x.astype(np.float64)
+        mag = np.abs(W) @ np.abs(x.astype(np.float64))
+        for blocked in (False, True):
+            got = O.matvec(w, wtype, x, in_dim, rows, blocked).astype(np.float64)
+            assert (np.abs(got - exact) <= (in_dim // 32 + 260) * u * mag).all(), (wtype, blocked)
+
+
+def test_rmsnorm_closed_forms():
+    # constant rows: every partial sum is exact, so inv_rms is the correctly
+    # rounded 1/sqrt(c^2 + eps); c = 1/2, eps = 0 gives exactly 2 and the
+    # output is the weight itself
+    dim = 2560
+    w = np.random.default_rng(34).standard_normal(dim).astype(np.float32)
+    h = np.full(dim, 0.5, dtype=np.float32)
+    assert np.array_equal(O.rmsnorm(h, w, 0.0), w)
+    for c, eps in ((3.0, 1e-6), (0.125, 1e-6), (1.0, 0.5)):
+        h = np.full(dim, c, dtype=np.float32)
+        inv = np.float32(1.0) / np.sqrt(np.float32(np.float32(c * c) + np.float32(eps)))
+        want = (h * inv) * w
+        assert np.array_equal(O.rmsnorm(h, w, eps), want)
+
+
+def test_rmsnorm_against_float64():
+    rng = np.random.default_rng(35)
+    for dim in (256, 2560, 1000):
+        h = (rng.standard_normal(dim) * 10.0).astype(np.float32)
+        w = rng.standard_normal(dim).astype(np.float32)
+        got = O.rmsnorm(h, w, 1e-6).astype(np.float64)
+        want = h.astype(np.float64) / np.sqrt(np.mean(h.astype(np.float64) ** 2) + 1e-6) * w
+        assert np.allclose(got, want, rtol=2e-6, atol=0), np.abs(got - want).max()

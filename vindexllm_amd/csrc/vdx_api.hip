@@ -392,34 +392,47 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
   return tok;
 }
 
-static const char *lmhead_check(const void *weights, const float *hidden, int32_t rows,
-                                int32_t in_dim, int32_t vocab) {
+static int lm_block_bytes(int32_t wtype) {
+  return wtype == kLmQ4_0 ? 18 : wtype == kLmQ8_0 ? 34 : wtype == kLmF16 ? 64 : 0;
+}
+
+// nullptr when the arguments are valid; *rc is set to the error code otherwise
+static const char *lmhead_check(const void *weights, int32_t wtype, const float *hidden, int32_t rows,
+                                int32_t in_dim, int32_t vocab, int *rc) {
+  *rc = VDX_E_INVALID_ARG;
   if (!weights || !hidden) return "lm_head: weights and hidden are required";
   if (rows <= 0 || vocab <= 0) return "lm_head: need rows > 0 and vocab > 0";
+  if (lm_block_bytes(wtype) == 0) {
+    *rc = VDX_E_UNSUPPORTED;
+    return "lm_head: weight type must be VDX_TENSOR_Q4_0, VDX_TENSOR_Q8_0 or VDX_TENSOR_F16";
+  }
   if (in_dim <= 0 || in_dim % 256 != 0) return "lm_head: in_dim must be a positive multiple of 256";
   if ((uintptr_t)weights % 16 != 0) return "lm_head: weights must be 16-byte aligned";
-  if ((int64_t)(in_dim / 32) * 18 * 256 > (int64_t)0x7FFFFFFF) return "lm_head: in_dim too large";
+  if ((int64_t)(in_dim / 32) * lm_block_bytes(wtype) * 64 > (int64_t)0x7FFFFFFF)
+    return "lm_head: in_dim too large";
+  *rc = VDX_OK;
   return nullptr;
 }
 
-int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
-                    int32_t vocab, float *logits, int64_t logit_stride, float *scratch,
-                    void *stream) {
-  if (const char *m = lmhead_check(weights, hidden, rows, in_dim, vocab)) {
+int vdx_lmhead(const void *weights, int32_t wtype, const float *hidden, const float *norm_weight,
+               float norm_eps, int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
+               int64_t logit_stride, float *scratch, void *stream) {
+  int rc = VDX_OK;
+  if (const char *m = lmhead_check(weights, wtype, hidden, rows, in_dim, vocab, &rc)) {
     g_call_err = m;
-    return VDX_E_INVALID_ARG;
+    return rc;
   }
   if (!logits || logit_stride < vocab) {
     g_call_err = "lm_head: logits required, logit_stride >= vocab";
     return VDX_E_INVALID_ARG;
   }
-  if (rows > 1 && !scratch) {
-    g_call_err = "lm_head: scratch (16*in_dim floats) is required when rows > 1";
+  if ((rows > 1 || norm_weight) && !scratch) {
+    g_call_err = "lm_head: scratch (16*in_dim floats) is required when rows > 1 or with the norm";
     return VDX_E_INVALID_ARG;
   }
-  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride,
-                  rows, in_dim, vocab, scratch};
-  const hipError_t e = launch_lmhead_q4_0(lp, (hipStream_t)stream);
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride, rows, in_dim,
+                  vocab, scratch, wtype, norm_weight, norm_eps};
+  const hipError_t e = launch_lmhead(lp, (hipStream_t)stream);
   if (e != hipSuccess) {
     g_call_err = std::string("lm_head launch: ") + hipGetErrorString(e);
     return VDX_E_HIP;
@@ -428,13 +441,21 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
   return VDX_OK;
 }
 
-int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const float *hidden,
-                                   int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
-                                   int64_t logit_stride, const float *uniforms,
-                                   const vdx_sample_outputs *out, void *stream) {
+int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int32_t in_dim,
+                    int32_t vocab, float *logits, int64_t logit_stride, float *scratch,
+                    void *stream) {
+  return vdx_lmhead(weights, kLmQ4_0, hidden, nullptr, 0.0f, rows, in_dim, vocab, logits, logit_stride,
+                    scratch, stream);
+}
+
+int vdx_sampler_lmhead_device(vdx_sampler *s, const void *weights, int32_t wtype, const float *hidden,
+                              const float *norm_weight, float norm_eps, int32_t rows, int32_t in_dim,
+                              int32_t vocab, float *logits, int64_t logit_stride, const float *uniforms,
+                              const vdx_sample_outputs *out, void *stream) {
   if (!s) return VDX_E_INVALID_ARG;
-  if (const char *m = lmhead_check(weights, hidden, rows, in_dim, vocab))
-    return fail(s, VDX_E_INVALID_ARG, m);
+  int rc = VDX_OK;
+  if (const char *m = lmhead_check(weights, wtype, hidden, rows, in_dim, vocab, &rc))
+    return fail(s, rc, m);
   if (rows > s->max_rows) return fail(s, VDX_E_INVALID_ARG, "lm_head: rows must be <= max_rows");
   if (!out || !out->tokens) return fail(s, VDX_E_INVALID_ARG, "lm_head: out->tokens is required");
   HIP_TRY(s, hipSetDevice(s->device));
@@ -455,7 +476,7 @@ int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const fl
   } else if (ls < vocab) {
     return fail(s, VDX_E_INVALID_ARG, "lm_head: logit_stride must be >= vocab");
   }
-  if (rows > 1 && in_dim > s->xt_dim) {
+  if ((rows > 1 || norm_weight) && in_dim > s->xt_dim) {
     HIP_TRY(s, hipStreamSynchronize(s->stream));
     HIP_TRY(s, hipDeviceSynchronize());
     (void)hipFree(s->d_xt);
@@ -464,9 +485,18 @@ int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const fl
     HIP_TRY(s, hipMalloc(&s->d_xt, sizeof(float) * 16 * (size_t)in_dim));
     s->xt_dim = in_dim;
   }
-  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab, s->d_xt};
-  HIP_TRY(s, launch_lmhead_q4_0(lp, (hipStream_t)stream));
+  LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab, s->d_xt,
+                  wtype, norm_weight, norm_eps};
+  HIP_TRY(s, launch_lmhead(lp, (hipStream_t)stream));
   return vdx_sampler_process_device(s, logits, rows, vocab, ls, uniforms, out, stream);
+}
+
+int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const float *hidden,
+                                   int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
+                                   int64_t logit_stride, const float *uniforms,
+                                   const vdx_sample_outputs *out, void *stream) {
+  return vdx_sampler_lmhead_device(s, weights, kLmQ4_0, hidden, nullptr, 0.0f, rows, in_dim, vocab, logits,
+                                   logit_stride, uniforms, out, stream);
 }
 
 int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token) {

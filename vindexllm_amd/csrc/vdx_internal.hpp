@@ -34,9 +34,12 @@ struct CallParams {
   uint32_t *tickets;
 };
 
-// Q4_0 lm_head: logits[r*logit_stride + v] for rows r < rows, v < vocab.
+// lm_head weight formats (GGML tensor type ids, GGUFReader.pas:34-42).
+constexpr int kLmF16 = 1, kLmQ4_0 = 2, kLmQ8_0 = 8;
+
+// lm_head: logits[r*logit_stride + v] for rows r < rows, v < vocab.
 struct LmHeadParams {
-  const uint8_t *weights;  // vocab x (in_dim/32) blocks of 18 bytes, 16-byte aligned
+  const uint8_t *weights;  // vocab rows in `format`, 16-byte aligned
   const float *hidden;     // rows x in_dim (row r at hidden + r*hidden_stride)
   int64_t hidden_stride;
   float *logits;
@@ -44,10 +47,13 @@ struct LmHeadParams {
   int32_t rows;
   int32_t in_dim;          // multiple of 256
   int32_t vocab;
-  float *scratch;          // >= 16 * in_dim floats when rows > 1 (element-major hidden copy)
+  float *scratch;          // >= 16 * in_dim floats when rows > 1 or norm_weight (prepared hidden copy)
+  int32_t format;          // kLmQ4_0, kLmQ8_0 or kLmF16
+  const float *norm_weight;  // output RMSNorm weight [in_dim] (nullable: no norm)
+  float norm_eps;
 };
 
-hipError_t launch_lmhead_q4_0(const LmHeadParams &p, hipStream_t st);
+hipError_t launch_lmhead(const LmHeadParams &p, hipStream_t st);
 hipError_t launch_penalty(const CallParams &p, hipStream_t st);
 hipError_t launch_greedy(const CallParams &p, hipStream_t st);
 hipError_t launch_topk(const CallParams &p, hipStream_t st);

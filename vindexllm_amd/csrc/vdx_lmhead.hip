@@ -1,69 +1,84 @@
-// vdx_lmhead.hip -- Q4_0 lm_head (the reference's shaders/matvec_q4_0.comp,
-// dispatched by TVdxAttention.DispatchMatVec, src/VindexLLM.Attention.pas:979-1025,
-// from TVdxModel.UnembedToLogits, src/VindexLLM.Model.pas:1258-1270) for gfx950.
+// vdx_lmhead.hip -- the lm_head of TVdxModel.UnembedToLogits
+// (src/VindexLLM.Model.pas:1258-1270) for gfx950: the output RMSNorm
+// (shaders/rmsnorm_copy.comp via TVdxLayerNorm.ApplyCopy,
+// src/VindexLLM.LayerNorm.pas:395-417) followed by the matrix-vector product in
+// the embedding tensor's own GGUF format, as TVdxAttention.DispatchMatVec
+// selects it (src/VindexLLM.Attention.pas:979-1025): shaders/matvec_q4_0.comp,
+// matvec_q8_0.comp or matvec_f16.comp.
 //
-// logits[b][v] = sum_e (nibble(v,e) - 8) * d(v, e/32) * hidden[b][e] for a batch
-// of up to 16 hidden rows, so the 377 MB of Gemma-3-4B lm_head weights
-// (262144 x 2560 in Q4_0) stream from HBM once per step whatever the batch.
+// logits[b][v] = sum_e W(v, e) * xn[b][e] for a batch of up to 16 hidden rows,
+// so the lm_head weights (377 MB for Gemma-3-4B's 262144 x 2560 in Q4_0) stream
+// from HBM once per step whatever the batch.
 //
-// Q4_0 row layout (GGUFReader.pas:264-281, matvec_q4_0.comp:7-15): blocks of
-// 18 bytes, an fp16 scale d then 16 bytes qs; qs[j] & 0xF is element j and
-// qs[j] >> 4 is element j + 16 of the block.
+// Row layouts (GGUFReader.pas:264-281 and the shaders' headers):
+//   Q4_0: blocks of 18 bytes, fp16 scale d then 16 bytes qs; qs[j] & 0xF is
+//         element j and qs[j] >> 4 element j + 16 of the block; W = (q - 8) d.
+//   Q8_0: blocks of 34 bytes, fp16 scale d then 32 int8 q; W = q d.
+//   F16:  in_dim fp16 values.
 //
 // Arithmetic (fixed, so the oracle restates it bit for bit): per (row, batch
-// row) and per block k in order, s = 0; s = fma(q_i - 8, x[32k + i], s) for
-// i = 0..31; acc = fma(d_k, s, acc).  Each product (q - 8) * x is exact
-// before its single rounding, as in the shader; the shader's own summation
-// order (64 strided lanes, then a tree) differs only at fp32 rounding level.
+// row) and per block k of 32 elements in order, s = 0; s = fma(w_i, x[32k + i],
+// s) for i = 0..31 with w_i = q_i - 8 (Q4_0), q_i (Q8_0) or the fp16 value
+// (F16), each product exact before its single rounding; then acc = fma(d_k, s,
+// acc) (d_k = 1 for F16).  The shaders' own summation orders (256 or 64
+// strided lanes, then a tree) differ only at fp32 rounding level.
+//
+// Output RMSNorm (optional, before the product), in the shader's order:
+// thread t of 256 sums h[e]^2 for e = t, t + 256, ... (product then sum),
+// the 256 partials reduce as a tree (stride 128, 64, ..., 1), inv_rms =
+// 1 / sqrt(ss / dim + eps) with IEEE division and square root, and
+// xn[e] = (h[e] * inv_rms) * w[e].
 //
 // Mapping: one thread per vocabulary row, one wave (64 rows) per workgroup.
-// The K dimension is streamed in slices of 8 blocks (144 bytes per row): the
-// wave loads its 64 rows' slice with coalesced 16-byte loads (piece P of the
-// 9 KB slice tile goes to lane P mod 64), stages it in LDS (144-byte row
-// stride: each lane's 16-byte reads of its own row are bank-conflict free)
-// and prefetches the next slice into registers while computing.  The hidden
+// The K dimension is streamed in slices (Q4_0: 8 blocks, 144 bytes per row;
+// Q8_0: 4 blocks, 136 bytes; F16: 64 values, 128 bytes): the wave loads its
+// 64 rows' slice with coalesced loads (piece P of the slice tile goes to lane
+// P mod 64), stages it in LDS (each lane then reads its own row) and
+// prefetches the next slice into registers while computing.  The hidden
 // values are the same for every lane, so they are read with scalar loads and
-// enter the FMAs as SGPR operands; with more than one batch row they are read
-// from a transposed copy (element-major, 16 batch rows per 64-byte line), so
-// one scalar load feeds the 16 independent accumulation chains of an element.
-// The weights are turned into f16 (q - 8) pairs (v_perm_b32 + one packed f16
-// subtract per two weights) that v_fma_mix_f32 consumes directly, so a
-// weight costs ~1.5 VALU ops of dequantisation plus one FMA per batch row.
+// enter the FMAs as SGPR operands; with more than one batch row (or the norm)
+// they are read from a prepared copy, element-major with 16 batch rows per
+// 64-byte line, so one scalar load feeds the independent accumulation chains
+// of an element.  Quantised weights become f16 pairs exactly (v_perm_b32 puts
+// each byte under a 0x64 byte, f16 1024 + u, and one packed f16 subtract
+// removes the offset) that v_fma_mix_f32 consumes directly.
 #include "vdx_internal.hpp"
 
 namespace vdx {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kLmPieces = 9;    // 16-byte pieces of one row per slice
-static_assert(kLmPieces * 16 == 8 * 18, "a slice is 8 Q4_0 blocks");
+// Per-format slice geometry: a slice holds NBLK blocks of 32 elements of a
+// row, moved as PIECES loads of PIECE_DW dwords.
+template <int FMT> struct LmFmt;
+template <> struct LmFmt<kLmQ4_0> {
+  static constexpr int kBlockBytes = 18, kNBlk = 8, kPieceDw = 4, kPieces = 9;
+};
+template <> struct LmFmt<kLmQ8_0> {
+  static constexpr int kBlockBytes = 34, kNBlk = 4, kPieceDw = 2, kPieces = 17;
+};
+template <> struct LmFmt<kLmF16> {
+  static constexpr int kBlockBytes = 64, kNBlk = 2, kPieceDw = 4, kPieces = 8;
+};
+template <int FMT> constexpr int slice_dw() { return LmFmt<FMT>::kPieces * LmFmt<FMT>::kPieceDw; }
+static_assert(9 * 16 == 8 * 18 && 17 * 8 == 4 * 34 && 8 * 16 == 2 * 64, "slices are whole blocks");
 
-// Two weights (q - 8) as f16 from bytes of `nib` (each 0..15): the selector
-// places one nibble byte under a 0x64 byte per half (f16 1024 + q), and the
-// subtraction of 1032 is exact.
-__device__ __forceinline__ f16x2 q4_pair(uint32_t nib, uint32_t sel) {
-  const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, nib, sel);
-  return __builtin_bit_cast(f16x2, bits) - (f16x2){(_Float16)1032.0f, (_Float16)1032.0f};
+// Two (byte + 128) values of `u` as f16 1024 + (byte + 128) (the selector
+// puts one byte of u under a 0x64 byte per half), minus `off`: exact.
+template <int OFF>
+__device__ __forceinline__ f16x2 byte_pair(uint32_t u, uint32_t sel) {
+  const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, u, sel);
+  return __builtin_bit_cast(f16x2, bits) - (f16x2){(_Float16)OFF, (_Float16)OFF};
 }
 
-// One block (qs dwords q[0..3], fp16 scale bits `dbits`) for NB batch rows;
-// x points at the block's first hidden value in the element-major layout
-// x[e * NB + b] (for NB == 1 the hidden row itself).
+// One block of 32 weights (as 16 f16 pairs) for NB batch rows; x points at
+// the block's first hidden value in the element-major layout x[e * NB + b]
+// (for NB == 1 the hidden row itself).
 template <int NB>
-__device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits,
-                                         const float *__restrict__ x, float (&acc)[NB]) {
-  f16x2 w[16];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = q[j] & 0x0F0F0F0Fu;
-    const uint32_t hi = (q[j] >> 4) & 0x0F0F0F0Fu;
-    w[2 * j] = q4_pair(lo, 0x04010400u);      // elements 4j, 4j+1
-    w[2 * j + 1] = q4_pair(lo, 0x04030402u);  // elements 4j+2, 4j+3
-    w[8 + 2 * j] = q4_pair(hi, 0x04010400u);  // elements 16+4j, 16+4j+1
-    w[9 + 2 * j] = q4_pair(hi, 0x04030402u);  // elements 16+4j+2, 16+4j+3
-  }
-  const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dbits & 0xFFFFu));
+__device__ __forceinline__ void block_fma(const f16x2 (&w)[16], float d, const float *__restrict__ x,
+                                          float (&acc)[NB]) {
   float s[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) s[b] = 0.0f;
@@ -75,54 +90,124 @@ __device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits,
   for (int b = 0; b < NB; ++b) acc[b] = __builtin_fmaf(d, s[b], acc[b]);
 }
 
-// One slice (8 blocks = 4 block pairs of 9 dwords) of a row.
+__device__ __forceinline__ float half_bits(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+}
+
+// Q4_0 block: qs dwords q[0..3], scale bits dbits.
 template <int NB>
-__device__ __forceinline__ void q4_slice(const uint32_t (&r)[4 * kLmPieces], const float *__restrict__ x,
+__device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits, const float *__restrict__ x,
                                          float (&acc)[NB]) {
+  f16x2 w[16];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t *pr = r + 9 * m;
-    // even block: scale in bytes 0-1, qs in bytes 2-17 (straddling dwords)
-    const uint32_t qa[4] = {__builtin_amdgcn_alignbyte(pr[1], pr[0], 2),
-                            __builtin_amdgcn_alignbyte(pr[2], pr[1], 2),
-                            __builtin_amdgcn_alignbyte(pr[3], pr[2], 2),
-                            __builtin_amdgcn_alignbyte(pr[4], pr[3], 2)};
-    q4_block<NB>(qa, pr[0], x + 64 * m * NB, acc);
-    // odd block: scale in bytes 18-19, qs in bytes 20-35 (dword aligned)
-    const uint32_t qb[4] = {pr[5], pr[6], pr[7], pr[8]};
-    q4_block<NB>(qb, pr[4] >> 16, x + (64 * m + 32) * NB, acc);
+  for (int j = 0; j < 4; ++j) {  // offset 1024 + 8
+    const uint32_t lo = q[j] & 0x0F0F0F0Fu;
+    const uint32_t hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+    w[2 * j] = byte_pair<1032>(lo, 0x04010400u);      // elements 4j, 4j+1
+    w[2 * j + 1] = byte_pair<1032>(lo, 0x04030402u);  // elements 4j+2, 4j+3
+    w[8 + 2 * j] = byte_pair<1032>(hi, 0x04010400u);  // elements 16+4j, 16+4j+1
+    w[9 + 2 * j] = byte_pair<1032>(hi, 0x04030402u);  // elements 16+4j+2, 16+4j+3
+  }
+  block_fma<NB>(w, half_bits(dbits), x, acc);
+}
+
+// Q8_0 block: qs dwords q[0..7] (four int8 each), scale bits dbits.
+template <int NB>
+__device__ __forceinline__ void q8_block(const uint32_t (&q)[8], uint32_t dbits, const float *__restrict__ x,
+                                         float (&acc)[NB]) {
+  f16x2 w[16];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {  // offset 1024 + 128
+    const uint32_t u = q[j] ^ 0x80808080u;  // signed byte + 128
+    w[2 * j] = byte_pair<1152>(u, 0x04010400u);
+    w[2 * j + 1] = byte_pair<1152>(u, 0x04030402u);
+  }
+  block_fma<NB>(w, half_bits(dbits), x, acc);
+}
+
+// One slice of a row (dwords r[]), element-major hidden values x.
+template <int FMT, int NB>
+__device__ __forceinline__ void lm_slice(const uint32_t (&r)[slice_dw<FMT>()], const float *__restrict__ x,
+                                         float (&acc)[NB]) {
+  if constexpr (FMT == kLmQ4_0) {
+    // 4 block pairs of 9 dwords: the even block's scale in bytes 0-1 and qs in
+    // bytes 2-17 (straddling dwords), the odd block's scale in bytes 18-19 and
+    // qs in bytes 20-35 (dword aligned)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t *pr = r + 9 * m;
+      const uint32_t qa[4] = {__builtin_amdgcn_alignbyte(pr[1], pr[0], 2),
+                              __builtin_amdgcn_alignbyte(pr[2], pr[1], 2),
+                              __builtin_amdgcn_alignbyte(pr[3], pr[2], 2),
+                              __builtin_amdgcn_alignbyte(pr[4], pr[3], 2)};
+      q4_block<NB>(qa, pr[0], x + 64 * m * NB, acc);
+      const uint32_t qb[4] = {pr[5], pr[6], pr[7], pr[8]};
+      q4_block<NB>(qb, pr[4] >> 16, x + (64 * m + 32) * NB, acc);
+    }
+  } else if constexpr (FMT == kLmQ8_0) {
+    // 2 block pairs of 17 dwords: the even block's scale in bytes 0-1 and qs
+    // in bytes 2-33, the odd block's scale in bytes 34-35 and qs in 36-67
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t *pr = r + 17 * m;
+      uint32_t qa[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qa[k] = __builtin_amdgcn_alignbyte(pr[k + 1], pr[k], 2);
+      q8_block<NB>(qa, pr[0], x + 64 * m * NB, acc);
+      uint32_t qb[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qb[k] = pr[9 + k];
+      q8_block<NB>(qb, pr[8] >> 16, x + (64 * m + 32) * NB, acc);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      f16x2 w[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) w[k] = __builtin_bit_cast(f16x2, r[16 * m + k]);
+      block_fma<NB>(w, 1.0f, x + 32 * m * NB, acc);
+    }
   }
 }
 
-// x: hidden row (NB == 1) or the element-major copy [in_dim][NB].
-template <int NB>
-__global__ __launch_bounds__(64) void k_lmhead_q4_0(const uint8_t *__restrict__ wq,
-                                                    const float *__restrict__ x,
-                                                    float *__restrict__ logits, int64_t ls,
-                                                    int32_t in_dim, int32_t vocab, int32_t B) {
-  __shared__ u32x4 tile[64 * kLmPieces];
+template <int FMT> struct PieceT;
+template <> struct PieceT<kLmQ4_0> { typedef u32x4 T; };
+template <> struct PieceT<kLmQ8_0> { typedef u32x2 T; };
+template <> struct PieceT<kLmF16> { typedef u32x4 T; };
+
+// x: hidden row (NB == 1, no norm) or the prepared copy [in_dim][NB].
+template <int FMT, int NB>
+__global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, const float *__restrict__ x,
+                                               float *__restrict__ logits, int64_t ls, int32_t in_dim,
+                                               int32_t vocab, int32_t B) {
+  typedef LmFmt<FMT> F;
+  typedef typename PieceT<FMT>::T Piece;
+  constexpr int P = F::kPieces, PD = F::kPieceDw, PB = 4 * PD;  // pieces, dwords and bytes per piece
+  constexpr int SE = 32 * F::kNBlk;                              // elements per slice
+  __shared__ Piece tile[64 * P];
   const int t = threadIdx.x;
   const int v0 = blockIdx.x * 64;
   const int nrows = min(64, vocab - v0);
-  const int rowbytes = (in_dim >> 5) * 18;
-  const int nslices = in_dim >> 8;
+  // unsigned arithmetic: in_dim > 0 (the signed forms cost registers here)
+  const int rowbytes = (int)(((uint32_t)in_dim >> 5) * (uint32_t)F::kBlockBytes);
+  const int nslices = (int)((uint32_t)in_dim / (uint32_t)SE);
   const uint8_t *wt = wq + (int64_t)v0 * rowbytes;
 
-  // piece P = t + 64 i of a slice tile is piece j = P % 9 of row P / 9; rows
+  // piece Q = t + 64 i of a slice tile is piece j = Q % P of row Q / P; rows
   // past the vocabulary read the tile's first row (their results are not
   // stored)
-  int goff[kLmPieces];
+  int goff[P];
 #pragma unroll
-  for (int i = 0; i < kLmPieces; ++i) {
-    const int P = t + 64 * i;
-    const int r = P / kLmPieces, j = P - r * kLmPieces;
-    goff[i] = (r < nrows) ? r * rowbytes + 16 * j : 0;
+  for (int i = 0; i < P; ++i) {
+    const int Q = t + 64 * i;
+    const int r = Q / P, j = Q - r * P;
+    goff[i] = (r < nrows) ? r * rowbytes + PB * j : 0;
   }
-  u32x4 pre[kLmPieces];
+  Piece pre[P];
   auto load_slice = [&](int s) {
 #pragma unroll
-    for (int i = 0; i < kLmPieces; ++i)
-      pre[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wt + goff[i] + 144 * s));
+    for (int i = 0; i < P; ++i)
+      pre[i] = __builtin_nontemporal_load(reinterpret_cast<const Piece *>(wt + goff[i] + P * PB * s));
   };
   load_slice(0);
 
@@ -132,19 +217,17 @@ __global__ __launch_bounds__(64) void k_lmhead_q4_0(const uint8_t *__restrict__ 
   for (int s = 0; s < nslices; ++s) {
     __syncthreads();  // the previous slice has been read (one wave: no-op ordering)
 #pragma unroll
-    for (int i = 0; i < kLmPieces; ++i) tile[t + 64 * i] = pre[i];
+    for (int i = 0; i < P; ++i) tile[t + 64 * i] = pre[i];
     __syncthreads();
     if (s + 1 < nslices) load_slice(s + 1);
-    uint32_t r[4 * kLmPieces];
+    uint32_t r[P * PD];
 #pragma unroll
-    for (int j = 0; j < kLmPieces; ++j) {
-      const u32x4 v = tile[t * kLmPieces + j];
-      r[4 * j] = v[0];
-      r[4 * j + 1] = v[1];
-      r[4 * j + 2] = v[2];
-      r[4 * j + 3] = v[3];
+    for (int j = 0; j < P; ++j) {
+      const Piece v = tile[t * P + j];
+#pragma unroll
+      for (int k = 0; k < PD; ++k) r[PD * j + k] = v[k];
     }
-    q4_slice<NB>(r, x + 256 * NB * s, acc);
+    lm_slice<FMT, NB>(r, x + SE * NB * s, acc);
   }
   if (t < nrows) {
 #pragma unroll
@@ -153,43 +236,78 @@ __global__ __launch_bounds__(64) void k_lmhead_q4_0(const uint8_t *__restrict__ 
   }
 }
 
-// Element-major copy of up to 16 hidden rows: xt[e * NB + b] = hidden[b][e]
-// (rows b >= B are zero).
-__global__ __launch_bounds__(256) void k_lmhead_xt(const float *__restrict__ hidden, int64_t hs,
-                                                   int32_t in_dim, int32_t B, int32_t NB,
-                                                   float *__restrict__ xt) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= in_dim * NB) return;
-  const int e = i / NB, b = i - e * NB;
-  xt[i] = (b < B) ? hidden[(int64_t)b * hs + e] : 0.0f;
+// The prepared hidden copy: xt[e * NB + b] = hidden[b][e], or with the norm
+// weight w the output RMSNorm of that row; rows b >= B are zero.  One
+// workgroup per b < NB.
+__global__ __launch_bounds__(256) void k_lmhead_prep(const float *__restrict__ hidden, int64_t hs,
+                                                     const float *__restrict__ w, float eps, int32_t in_dim,
+                                                     int32_t B, int32_t NB, float *__restrict__ xt) {
+  __shared__ float part[256];
+  const int b = blockIdx.x, t = threadIdx.x;
+  if (b >= B) {
+    for (int e = t; e < in_dim; e += 256) xt[(int64_t)e * NB + b] = 0.0f;
+    return;
+  }
+  const float *h = hidden + (int64_t)b * hs;
+  if (!w) {
+    for (int e = t; e < in_dim; e += 256) xt[(int64_t)e * NB + b] = h[e];
+    return;
+  }
+  float ss = 0.0f;
+  for (int e = t; e < in_dim; e += 256) {
+    const float v = h[e];
+    ss = ss + v * v;  // product, then sum (no contraction in this build)
+  }
+  part[t] = ss;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (t < stride) part[t] = part[t] + part[t + stride];
+    __syncthreads();
+  }
+  // fl32(sqrt(q)) and fl32(1 / s) through double operations: both double
+  // roundings are innocuous (53 >= 2 * 24 + 2 bits), so these are the
+  // correctly rounded fp32 square root and reciprocal
+  const float q = part[0] / (float)in_dim + eps;
+  const float sq = (float)__builtin_sqrt((double)q);
+  const float inv_rms = (float)(1.0 / (double)sq);
+  for (int e = t; e < in_dim; e += 256) xt[(int64_t)e * NB + b] = (h[e] * inv_rms) * w[e];
 }
 
-hipError_t launch_lmhead_q4_0(const LmHeadParams &p, hipStream_t st) {
+template <int FMT>
+static void launch_fmt(int NB, dim3 grid, hipStream_t st, const uint8_t *w, const float *x, float *l,
+                       int64_t ls, int32_t in_dim, int32_t vocab, int32_t B) {
+#define VDX_LM(N) hipLaunchKernelGGL((k_lmhead<FMT, N>), grid, dim3(64), 0, st, w, x, l, ls, in_dim, vocab, B)
+  if (NB == 1)
+    VDX_LM(1);
+  else if (NB == 2)
+    VDX_LM(2);
+  else if (NB == 4)
+    VDX_LM(4);
+  else if (NB == 8)
+    VDX_LM(8);
+  else
+    VDX_LM(16);
+#undef VDX_LM
+}
+
+hipError_t launch_lmhead(const LmHeadParams &p, hipStream_t st) {
   const dim3 grid((unsigned)((p.vocab + 63) / 64));
   for (int b0 = 0; b0 < p.rows; b0 += 16) {
     const int B = min(16, p.rows - b0);
     const float *x = p.hidden + (int64_t)b0 * p.hidden_stride;
     float *l = p.logits + (int64_t)b0 * p.logit_stride;
     const int NB = (B == 1) ? 1 : (B == 2) ? 2 : (B <= 4) ? 4 : (B <= 8) ? 8 : 16;
-    if (NB > 1) {
-      hipLaunchKernelGGL(k_lmhead_xt, dim3((unsigned)((p.in_dim * NB + 255) / 256)), dim3(256), 0,
-                         st, x, p.hidden_stride, p.in_dim, B, NB, p.scratch);
+    if (NB > 1 || p.norm_weight) {
+      hipLaunchKernelGGL(k_lmhead_prep, dim3((unsigned)NB), dim3(256), 0, st, x, p.hidden_stride,
+                         p.norm_weight, p.norm_eps, p.in_dim, B, NB, p.scratch);
       x = p.scratch;
     }
-#define VDX_LM(N)                                                                           \
-  hipLaunchKernelGGL(k_lmhead_q4_0<N>, grid, dim3(64), 0, st, p.weights, x, l, p.logit_stride, \
-                     p.in_dim, p.vocab, B)
-    if (NB == 1)
-      VDX_LM(1);
-    else if (NB == 2)
-      VDX_LM(2);
-    else if (NB == 4)
-      VDX_LM(4);
-    else if (NB == 8)
-      VDX_LM(8);
+    if (p.format == kLmQ4_0)
+      launch_fmt<kLmQ4_0>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
+    else if (p.format == kLmQ8_0)
+      launch_fmt<kLmQ8_0>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
     else
-      VDX_LM(16);
-#undef VDX_LM
+      launch_fmt<kLmF16>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

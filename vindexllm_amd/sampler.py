@@ -27,6 +27,10 @@ VDX_E_NO_MEMORY = -4
 VDX_RNG_XOSHIRO = 0
 VDX_RNG_PHILOX = 1
 
+VDX_TENSOR_F16 = 1   # lm_head weight formats: GGML type ids (GGUFReader.pas:34-42)
+VDX_TENSOR_Q4_0 = 2
+VDX_TENSOR_Q8_0 = 8
+
 ROW_GREEDY = 0x1
 ROW_TOPK_FAST = 0x2
 ROW_TOPK_REPLAY = 0x4
@@ -86,6 +90,11 @@ _SIGNATURES = {
                                              C.c_void_p]),
     "vdx_lmhead_q4_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                   C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "vdx_lmhead": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_float, C.c_int32,
+                             C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "vdx_sampler_lmhead_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                            C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                            C.c_int64, C.c_void_p, C.POINTER(_Outputs), C.c_void_p]),
     "vdx_sampler_lmhead_q4_0_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                                  C.c_int32, C.c_int32, C.c_void_p, C.c_int64,
                                                  C.c_void_p, C.POINTER(_Outputs), C.c_void_p]),
@@ -244,14 +253,16 @@ class TVdxSampler:
             C.c_void_p(st.cuda_stream)))
         return tokens
 
-    def lmhead_q4_0_device(self, weights, hidden, vocab: int, logits=None, uniforms=None,
-                           tokens=None, topk_idx=None, topk_prob=None, flags=None,
-                           uniforms_out=None, stream=None):
-        """RunUnembedding + Process (Inference.pas:327-339) on the GPU: the Q4_0
-        lm_head (``weights``: uint8 GPU tensor, vocab rows of in_dim/32 18-byte
-        blocks) over ``hidden`` (rows x in_dim float32 GPU tensor) writes logits
-        into ``logits`` (rows x >= vocab float32 GPU tensor) or the sampler's
-        workspace, and the rows are sampled as by ``process_device``."""
+    def lmhead_device(self, weights, wtype: int, hidden, vocab: int, norm_weight=None,
+                      norm_eps: float = 1e-6, logits=None, uniforms=None, tokens=None,
+                      topk_idx=None, topk_prob=None, flags=None, uniforms_out=None, stream=None):
+        """RunUnembedding + Process (Inference.pas:327-339) on the GPU: the output
+        RMSNorm (``norm_weight``, float32 GPU tensor of in_dim; None skips it)
+        and the lm_head in ``wtype`` (VDX_TENSOR_Q4_0 / _Q8_0 / _F16; ``weights``:
+        uint8 GPU tensor, vocab rows in that GGUF layout) over ``hidden`` (rows x
+        in_dim float32 GPU tensor) write logits into ``logits`` (rows x >= vocab
+        float32 GPU tensor) or the sampler's workspace, and the rows are sampled
+        as by ``process_device``."""
         import torch
 
         assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.is_contiguous()
@@ -273,14 +284,27 @@ class TVdxSampler:
         if logits is not None:
             assert logits.is_cuda and logits.dtype == torch.float32
             lp, ls = C.c_void_p(logits.data_ptr()), int(logits.stride(0))
+        nw = None
+        if norm_weight is not None:
+            assert norm_weight.is_cuda and norm_weight.dtype == torch.float32 and norm_weight.numel() >= D
+            nw = C.c_void_p(norm_weight.data_ptr())
         st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
-        self._check(load_library().vdx_sampler_lmhead_q4_0_device(
-            self._h, C.c_void_p(weights.data_ptr()), C.c_void_p(hidden.data_ptr()), B, D,
-            int(vocab), lp, ls, C.c_void_p(uniforms.data_ptr()) if uniforms is not None else None,
-            C.byref(o), C.c_void_p(st.cuda_stream)))
+        self._check(load_library().vdx_sampler_lmhead_device(
+            self._h, C.c_void_p(weights.data_ptr()), int(wtype), C.c_void_p(hidden.data_ptr()), nw,
+            float(norm_eps), B, D, int(vocab), lp, ls,
+            C.c_void_p(uniforms.data_ptr()) if uniforms is not None else None, C.byref(o),
+            C.c_void_p(st.cuda_stream)))
         return tokens
 
-    # -- instrumentation ------------------------------------------------------
+    def lmhead_q4_0_device(self, weights, hidden, vocab: int, logits=None, uniforms=None,
+                           tokens=None, topk_idx=None, topk_prob=None, flags=None,
+                           uniforms_out=None, stream=None):
+        """lmhead_device for a Q4_0 head without the output norm."""
+        return self.lmhead_device(weights, VDX_TENSOR_Q4_0, hidden, vocab, logits=logits,
+                                  uniforms=uniforms, tokens=tokens, topk_idx=topk_idx,
+                                  topk_prob=topk_prob, flags=flags, uniforms_out=uniforms_out,
+                                  stream=stream)
+
     def set_timing(self, enable: bool):
         self._check(load_library().vdx_sampler_set_timing(self._h, 1 if enable else 0))
 
@@ -327,10 +351,13 @@ class TVdxSampler:
         return buf[:n].tolist(), pos.value
 
 
-def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=None):
-    """The Q4_0 lm_head alone (matvec_q4_0.comp, batched): returns the rows x
-    vocab float32 logits tensor (or fills ``logits``).  ``scratch`` (float32
-    GPU tensor of >= 16*in_dim elements) is allocated here when not given."""
+def lmhead(weights, wtype: int, hidden, vocab: int, norm_weight=None, norm_eps: float = 1e-6,
+           logits=None, scratch=None, stream=None):
+    """UnembedToLogits alone (Model.pas:1258-1270): the optional output RMSNorm
+    then the lm_head in ``wtype`` (VDX_TENSOR_Q4_0 / _Q8_0 / _F16), batched over
+    the rows of ``hidden``; returns the rows x vocab float32 logits tensor (or
+    fills ``logits``).  ``scratch`` (float32 GPU tensor of >= 16*in_dim) is
+    allocated here when needed and not given."""
     import torch
 
     assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.is_contiguous()
@@ -340,17 +367,26 @@ def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=N
     B, D = int(hidden.shape[0]), int(hidden.shape[1])
     if logits is None:
         logits = torch.empty(B, int(vocab), dtype=torch.float32, device=hidden.device)
-    if scratch is None and B > 1:
+    if scratch is None and (B > 1 or norm_weight is not None):
         scratch = torch.empty(16 * D, dtype=torch.float32, device=hidden.device)
+    nw = None
+    if norm_weight is not None:
+        assert norm_weight.is_cuda and norm_weight.dtype == torch.float32 and norm_weight.numel() >= D
+        nw = C.c_void_p(norm_weight.data_ptr())
     st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
-    rc = load_library().vdx_lmhead_q4_0(C.c_void_p(weights.data_ptr()),
-                                         C.c_void_p(hidden.data_ptr()), B, D, int(vocab),
-                                         C.c_void_p(logits.data_ptr()), int(logits.stride(0)),
-                                         C.c_void_p(scratch.data_ptr()) if scratch is not None
-                                         else None, C.c_void_p(st.cuda_stream))
+    rc = load_library().vdx_lmhead(C.c_void_p(weights.data_ptr()), int(wtype),
+                                   C.c_void_p(hidden.data_ptr()), nw, float(norm_eps), B, D,
+                                   int(vocab), C.c_void_p(logits.data_ptr()), int(logits.stride(0)),
+                                   C.c_void_p(scratch.data_ptr()) if scratch is not None else None,
+                                   C.c_void_p(st.cuda_stream))
     if rc != VDX_OK:
         raise VdxSamplerError(rc, _err(None))
     return logits
+
+
+def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=None):
+    """The Q4_0 lm_head alone (matvec_q4_0.comp, batched), without the norm."""
+    return lmhead(weights, VDX_TENSOR_Q4_0, hidden, vocab, logits=logits, scratch=scratch, stream=stream)
 
 
 def version() -> str:
