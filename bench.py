@@ -220,26 +220,36 @@ LMHEAD_V, LMHEAD_D = 262144, 2560  # Gemma-3-4B tied lm_head (token_embd.weight)
 VALU_FP32_PEAK_TFLOPS = 157.3      # MI355X published FP32 vector peak (packed FMA)
 
 
-def run_lmhead(B, steps, warmup):
+LMHEAD_FORMATS = {"q4_0": (2, 18), "q8_0": (8, 34), "f16": (1, 64)}  # GGML type id, bytes per 32
+
+
+def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False):
     """lm_head + sampling with the logits kept in HBM (RunUnembedding followed
-    by Process, Inference.pas:327-339): the Q4_0 lm_head of 262144 x 2560
-    (nibbles uniform 0..15, fp16 scales |N(0, 0.02)|) over B hidden rows
-    N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  Times the whole call (both
-    kernels) and the lm_head kernel alone, each from a captured hipGraph."""
+    by Process, Inference.pas:327-339): the lm_head of 262144 x 2560 in `fmt`
+    (Q4_0: nibbles uniform 0..15; Q8_0: int8 uniform; fp16 scales
+    |N(0, 0.02)|; F16: N(0, 0.05)), optionally after the output RMSNorm, over
+    B hidden rows N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  Times the
+    whole call and the lm_head alone (norm included), each from a captured
+    hipGraph."""
     import torch
 
-    from vindexllm_amd import TVdxSampler, lmhead_q4_0
+    from vindexllm_amd import TVdxSampler, lmhead
 
     V, D = LMHEAD_V, LMHEAD_D
+    wtype, bb = LMHEAD_FORMATS[fmt]
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1005)
     nb = D // 32
-    w = torch.randint(0, 256, (V, nb, 18), dtype=torch.uint8, device=dev, generator=g)
-    d = (torch.randn(V, nb, device=dev, generator=g) * 0.02).abs().half()
-    w[:, :, 0:2] = d.view(torch.uint8).view(V, nb, 2)
-    w = w.view(-1)
+    if fmt == "f16":
+        w = (torch.randn(V, D, device=dev, generator=g) * 0.05).half().view(torch.uint8)
+    else:
+        w = torch.randint(0, 256, (V, nb, bb), dtype=torch.uint8, device=dev, generator=g)
+        d = (torch.randn(V, nb, device=dev, generator=g) * 0.02).abs().half()
+        w[:, :, 0:2] = d.view(torch.uint8).view(V, nb, 2)
+    w = w.reshape(-1)
     hidden = torch.randn(B, D, device=dev, generator=g)
+    nw = (1.0 + 0.1 * torch.randn(D, device=dev, generator=g)) if norm else None
     logits = torch.empty(B, V, dtype=torch.float32, device=dev)
     scratch = torch.empty(16 * D, dtype=torch.float32, device=dev)
     tok = torch.empty(B, dtype=torch.int32, device=dev)
@@ -251,10 +261,10 @@ def run_lmhead(B, steps, warmup):
     cs.wait_stream(torch.cuda.current_stream(dev))
 
     def both():
-        s.lmhead_q4_0_device(w, hidden, V, logits=logits, tokens=tok, stream=cs)
+        s.lmhead_device(w, wtype, hidden, V, norm_weight=nw, logits=logits, tokens=tok, stream=cs)
 
     def head():
-        lmhead_q4_0(w, hidden, V, logits=logits, scratch=scratch, stream=cs)
+        lmhead(w, wtype, hidden, V, norm_weight=nw, logits=logits, scratch=scratch, stream=cs)
 
     res = {}
     for tag, fn in (("call", both), ("lmhead", head)):
@@ -281,7 +291,7 @@ def run_lmhead(B, steps, warmup):
                         event_us=1e3 * e0.elapsed_time(e1) / steps)
     s.Free()
     head_us = res["lmhead"]["event_us"]
-    weight_bytes = V * nb * 18
+    weight_bytes = V * nb * bb
     alg_bytes = weight_bytes + B * D * 4
     flops = 2.0 * V * D * B
     out = {"rows_per_s": B / (res["call"]["wall_us"] * 1e-6),
@@ -293,7 +303,8 @@ def run_lmhead(B, steps, warmup):
            "lmhead_tflops": flops / (head_us * 1e-6) / 1e12,
            "lmhead_valu_frac": flops / (head_us * 1e-6) / 1e12 / VALU_FP32_PEAK_TFLOPS,
            "bound": "hbm" if B == 1 else "valu",
-           "desc": f"Q4_0 lm_head {V}x{D} + top-k 64/top-p 0.95, B={B} hidden rows N(0,1)"}
+           "desc": f"{fmt.upper()} lm_head {V}x{D}{' + output RMSNorm' if norm else ''} + top-k 64/top-p 0.95, "
+                   f"B={B} hidden rows N(0,1)"}
     return out
 
 
@@ -384,7 +395,9 @@ def main():
     ap.add_argument("--others", action="store_true", help="also measure the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--lmhead", type=int, metavar="B",
-                    help="only the Q4_0 lm_head + sampling workload at B hidden rows (one JSON line)")
+                    help="only the lm_head + sampling workload at B hidden rows (one JSON line)")
+    ap.add_argument("--lmhead-format", default="q4_0", choices=sorted(LMHEAD_FORMATS))
+    ap.add_argument("--lmhead-norm", action="store_true", help="fuse the output RMSNorm")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU: turn two rocprofv3 --pmc counter CSVs into profiles/traffic_<workload>.json")
     a = ap.parse_args()
@@ -397,7 +410,8 @@ def main():
         sys.exit(3)
 
     if a.lmhead:
-        print(json.dumps(run_lmhead(a.lmhead, min(a.steps, 500), min(a.warmup, 20))), flush=True)
+        print(json.dumps(run_lmhead(a.lmhead, min(a.steps, 500), min(a.warmup, 20), fmt=a.lmhead_format,
+                                    norm=a.lmhead_norm)), flush=True)
         return
     r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
@@ -441,6 +455,8 @@ def main():
                             / HBM_PEAK_GBS}
         for B in (1, 16):
             others[f"lmhead_b{B}"] = run_lmhead(B, 200, 10)
+        for fmt in ("q8_0", "f16"):
+            others[f"lmhead_{fmt}_norm_b1"] = run_lmhead(1, 200, 10, fmt=fmt, norm=True)
         out["other_workloads"] = others
     if a.copy_calibration:
         copy_calibration()
