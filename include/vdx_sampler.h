@@ -168,6 +168,63 @@ int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const fl
                                    int64_t logit_stride, const float *uniforms,
                                    const vdx_sample_outputs *out, void *stream);
 
+/* ---- GGUF model files (TVdxGGUFReader, GGUFReader.pas) ---------------------
+ * The lm_head's inputs come from the model file: `token_embd.weight` (the
+ * tied lm_head, Model.Gemma3.pas:180-198, in its GGUF layout as vdx_lmhead
+ * reads it), `output_norm.weight` (:174) and the dimensions.  The file is
+ * memory-mapped read-only and parsed as the reader does (header, metadata,
+ * tensor directory, aligned data section: GGUFReader.pas:605-745); a
+ * malformed file is an error (message in vdx_gguf_last_error), never a fault. */
+typedef struct vdx_gguf vdx_gguf;
+typedef struct vdx_gguf_tensor {
+  int32_t type;          /* GGML type id (VDX_TENSOR_* among them)          */
+  int32_t n_dims;
+  uint64_t dims[4];      /* dims[0] varies fastest (the row length)          */
+  uint64_t nbytes;       /* VdxGGMLTensorBytes (GGUFReader.pas:264-318); 0
+                            for types it does not size                      */
+  uint64_t file_offset;
+  const void *data;      /* host pointer into the mapping, valid until close */
+} vdx_gguf_tensor;
+
+typedef struct vdx_gguf_info {
+  uint32_t version;        /* GetVersion (GGUFReader.pas:747)                 */
+  uint32_t alignment;      /* GetAlignment (:762); general.alignment or 32    */
+  uint64_t tensor_count;   /* GetTensorCount (:752)                           */
+  uint64_t metadata_count; /* GetMetadataCount (:757), as the header states   */
+  uint64_t file_size;      /* GetFileSize (:767)                              */
+  uint64_t data_offset;    /* file offset of the tensor data (:727-745)       */
+} vdx_gguf_info;
+
+/* TVdxGGUFReader.Open (GGUFReader.pas:376-430): map and parse; *out is NULL
+ * on failure, with the message in vdx_gguf_last_error(NULL). */
+int vdx_gguf_open(vdx_gguf **out, const char *path);
+/* TVdxGGUFReader.Close (:360): unmaps; every data pointer becomes invalid. */
+void vdx_gguf_close(vdx_gguf *g);
+const char *vdx_gguf_last_error(const vdx_gguf *g);
+int vdx_gguf_get_info(const vdx_gguf *g, vdx_gguf_info *out);
+/* GetTensorList (:878): name of tensor `index` in directory order into buf
+ * (NUL-terminated, truncated to cap-1); returns the full length. */
+int vdx_gguf_tensor_name(const vdx_gguf *g, int64_t index, char *buf, int32_t cap);
+/* GetTensorInfo + GetTensorDataPtr (:847-876) for `name`: VDX_E_INVALID_ARG
+ * when absent; VDX_E_UNSUPPORTED when its bytes would run past the end of the
+ * file (type, dims and file_offset filled, data NULL). */
+int vdx_gguf_find_tensor(vdx_gguf *g, const char *name, vdx_gguf_tensor *out);
+/* GetMetadataKeys (:826): distinct key `index` in file order into buf;
+ * returns the full length. */
+int vdx_gguf_meta_key(const vdx_gguf *g, int64_t index, char *buf, int32_t cap);
+/* HasMetadata (:774) / TVdxGGUFMetaValue.ValueType: the GGUF value type
+ * (0..12) of `key`, or VDX_E_INVALID_ARG when absent. */
+int vdx_gguf_meta_type(const vdx_gguf *g, const char *key);
+/* Metadata values (GetMetadata, :779): integers of any width and bools as
+ * int64, floats of either width as double, strings copied into buf
+ * (NUL-terminated; returns the full length), arrays as element type and
+ * length (tokenizer.ggml.tokens gives the vocabulary size, Tokenizer.pas:124).
+ * A key of another type is VDX_E_INVALID_ARG. */
+int vdx_gguf_meta_int(vdx_gguf *g, const char *key, int64_t *out);
+int vdx_gguf_meta_float(vdx_gguf *g, const char *key, double *out);
+int vdx_gguf_meta_string(vdx_gguf *g, const char *key, char *buf, int32_t cap);
+int vdx_gguf_meta_array(vdx_gguf *g, const char *key, int32_t *elem_type, int64_t *length);
+
 /* TVdxSampler.AddToHistory (Sampler.pas:530-539) for one row. */
 int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token);
 

@@ -281,3 +281,41 @@ def test_lmhead_device_q8_0_norm_sampling():
     orc = oracle_rows(Lg, cfg, u)
     compare(g, orc, cfg, check_logits=False, label="Q8_0+norm B=4")
     log("[done] Q8_0 + RMSNorm lm_head + sampling")
+
+
+@pytest.mark.parametrize("wtype", [O.TENSOR_Q4_0, O.TENSOR_Q8_0, O.TENSOR_F16])
+def test_lmhead_from_gguf_file(tmp_path, wtype):
+    # token_embd.weight and output_norm.weight read from a model file by the
+    # library's GGUF reader, copied to the device unchanged, and run through
+    # the fused norm + lm_head: bit-exact with the oracle on the same bytes
+    import torch
+
+    import ggufw
+
+    from vindexllm_amd import TVdxGGUFReader, lm_head_from_gguf, lmhead
+
+    V, D, B = 4096 + 77, 2560, 3
+    log(f"[case] lm_head from GGUF wtype={wtype} V={V} D={D} B={B}")
+    rng = np.random.default_rng(9100 + wtype)
+    w = {O.TENSOR_Q8_0: rand_q8_0, O.TENSOR_F16: rand_f16, O.TENSOR_Q4_0: rand_q4_0}[wtype](rng, V, D)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    blob, _ = ggufw.build([("general.architecture", ggufw.STR, "gemma3"),
+                           ("general.alignment", ggufw.U32, 64)],
+                          [("output_norm.weight", [D], 0, nw.tobytes()),
+                           ("token_embd.weight", [D, V], wtype, w.tobytes())], alignment=64)
+    p = tmp_path / "head.gguf"
+    p.write_bytes(blob)
+    H = (rng.standard_normal((B, D)) * 3.0).astype(np.float32)
+    r = TVdxGGUFReader()
+    assert r.Open(str(p)), r.GetErrors()
+    dev = torch.device("cuda:0")
+    lm = lm_head_from_gguf(r, dev)
+    assert (lm["wtype"], lm["in_dim"], lm["vocab"]) == (wtype, D, V)
+    out = lmhead(lm["weights"], lm["wtype"], torch.from_numpy(H).to(dev), lm["vocab"],
+                 norm_weight=lm["norm_weight"], norm_eps=lm["norm_eps"])
+    torch.cuda.synchronize()
+    G = out.cpu().numpy()
+    for b in range(B):
+        want = O.matvec(w, wtype, O.rmsnorm(H[b], nw, 1e-6), D, V, True)
+        assert np.array_equal(G[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"[done] lm_head from GGUF wtype={wtype}")

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libvdxsampler.so")
-SOURCES = ["vdx_api.hip", "vdx_kernels.hip", "vdx_lmhead.hip"]
+SOURCES = ["vdx_api.hip", "vdx_kernels.hip", "vdx_lmhead.hip", "vdx_gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [

@@ -75,6 +75,28 @@ class _Outputs(C.Structure):
     ]
 
 
+class _GGUFInfo(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("alignment", C.c_uint32),
+        ("tensor_count", C.c_uint64),
+        ("metadata_count", C.c_uint64),
+        ("file_size", C.c_uint64),
+        ("data_offset", C.c_uint64),
+    ]
+
+
+class _GGUFTensor(C.Structure):
+    _fields_ = [
+        ("type", C.c_int32),
+        ("n_dims", C.c_int32),
+        ("dims", C.c_uint64 * 4),
+        ("nbytes", C.c_uint64),
+        ("file_offset", C.c_uint64),
+        ("data", C.c_void_p),
+    ]
+
+
 _lib = None
 
 # Every entry point declared in include/vdx_sampler.h, with its ctypes signature.
@@ -110,6 +132,19 @@ _SIGNATURES = {
     "vdx_sampler_set_timing": (C.c_int, [C.c_void_p, C.c_int32]),
     "vdx_sampler_get_timing": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_double),
                                          C.POINTER(C.c_int64)]),
+    "vdx_gguf_open": (C.c_int, [C.POINTER(C.c_void_p), C.c_char_p]),
+    "vdx_gguf_close": (None, [C.c_void_p]),
+    "vdx_gguf_last_error": (C.c_char_p, [C.c_void_p]),
+    "vdx_gguf_get_info": (C.c_int, [C.c_void_p, C.POINTER(_GGUFInfo)]),
+    "vdx_gguf_tensor_name": (C.c_int, [C.c_void_p, C.c_int64, C.c_char_p, C.c_int32]),
+    "vdx_gguf_find_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(_GGUFTensor)]),
+    "vdx_gguf_meta_key": (C.c_int, [C.c_void_p, C.c_int64, C.c_char_p, C.c_int32]),
+    "vdx_gguf_meta_type": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "vdx_gguf_meta_int": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]),
+    "vdx_gguf_meta_float": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_double)]),
+    "vdx_gguf_meta_string": (C.c_int, [C.c_void_p, C.c_char_p, C.c_char_p, C.c_int32]),
+    "vdx_gguf_meta_array": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int32),
+                                      C.POINTER(C.c_int64)]),
     "vdx_sampler_last_error": (C.c_char_p, [C.c_void_p]),
     "vdx_sampler_version": (C.c_char_p, []),
 }
