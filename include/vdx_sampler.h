@@ -81,11 +81,25 @@ int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows);
 void vdx_sampler_destroy(vdx_sampler *s);
 
 /* TVdxSampler.SetConfig (Sampler.pas:132-150): a RepeatWindow change resizes
- * and clears every row's history; a Seed change reseeds every row. */
+ * and clears every row's history; a Seed change reseeds every row (row r as a
+ * sampler with Seed + r).  Rows given their own configs take this one again:
+ * those whose window differs lose their history, those with their own seed
+ * are reseeded as row r. */
 int vdx_sampler_set_config(vdx_sampler *s, const vdx_sampler_config *cfg);
 
-/* TVdxSampler.GetConfig (Sampler.pas:152-155). */
+/* TVdxSampler.GetConfig (Sampler.pas:152-155): the sampler-wide config. */
 int vdx_sampler_get_config(const vdx_sampler *s, vdx_sampler_config *out);
+
+/* SetConfig for one row (Sampler.pas:132-150 applied to that row): a batch
+ * of independent sequences in one sampler, each with its own temperature,
+ * Top-K/Top-P/Min-P, penalty, window and seed (the reference holds one
+ * sequence per sampler, Sampler.pas:37-91).  A changed RepeatWindow clears the
+ * row's history; a changed Seed reseeds the row from Seed itself (a timer
+ * value for 0), so it draws what a reference sampler with this config draws.
+ * One call samples rows of different paths (greedy, top-K, full) together.
+ * Waits for the device to be idle. */
+int vdx_sampler_set_row_config(vdx_sampler *s, int32_t row, const vdx_sampler_config *cfg);
+int vdx_sampler_get_row_config(const vdx_sampler *s, int32_t row, vdx_sampler_config *out);
 
 /* TVdxSampler.Process (Sampler.pas:265-528) for one host-resident row, as
  * called by TVdxInference.RunUnembedding (Inference.pas:327-339): uploads the
@@ -246,6 +260,19 @@ int vdx_sampler_set_history(vdx_sampler *s, int32_t row, const int32_t *ids,
 /* Reads a row's history ring back (up to `cap` ids); returns the count. */
 int32_t vdx_sampler_get_history(vdx_sampler *s, int32_t row, int32_t *ids,
                                 int32_t cap, int32_t *pos);
+
+/* Sampler-state checkpoint of one row: its config, RNG state (xoshiro256**
+ * words, Philox counter and key) and history ring as one self-contained blob
+ * (the reference's SaveKVCache / LoadKVCache, Inference.pas:750-900, keep no
+ * sampler state, so a restored session draws a different stream).  Waits for
+ * the calls issued so far.  Returns the blob's size; nothing is written when
+ * buf is NULL or cap is smaller. */
+int64_t vdx_sampler_save_row_state(vdx_sampler *s, int32_t row, void *buf, int64_t cap);
+
+/* Restores a blob from vdx_sampler_save_row_state into `row` of this or
+ * another sampler with the same RNG kind: the row then continues exactly as
+ * the saved one would have (its config becomes the row's own). */
+int vdx_sampler_load_row_state(vdx_sampler *s, int32_t row, const void *buf, int64_t size);
 
 /* Selects VDX_RNG_XOSHIRO (default) or VDX_RNG_PHILOX; reseeds all rows. */
 int vdx_sampler_set_rng(vdx_sampler *s, int32_t kind);

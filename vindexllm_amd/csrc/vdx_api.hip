@@ -27,7 +27,13 @@ struct vdx_sampler {
   hipStream_t stream = nullptr;
   RowState *d_rows = nullptr;
   int32_t *d_hist = nullptr;
-  int32_t hist_len = 0;
+  int32_t hist_len = 0;     // ring stride: >= every row's window
+  // rows with their own configs (vdx_sampler_set_row_config)
+  bool per_row = false;
+  std::vector<vdx_sampler_config> row_cfg;  // every row's config (= cfg without per-row configs)
+  std::vector<uint8_t> own_seed;            // row seeded from its own Seed (else seed_base + row)
+  std::vector<uint64_t> own_seed_val;       // that seed, resolved (timer value for Seed = 0)
+  RowCfg *d_rcfg = nullptr;
   // workspace (sized for ws_chunks chunks per row)
   int32_t ws_chunks = 0;
   ChunkMeta *d_meta = nullptr;
@@ -80,14 +86,32 @@ static uint64_t timer_seed() {
 
 static int32_t chunks_for(int32_t vocab) { return (vocab + kChunk - 1) / kChunk; }
 
-// Reseeds rows [0, max_rows): SeedPRNG (Sampler.pas:224-241) with Seed + row.
+// Reseeds row `row` the way its config says: from its own resolved Seed, or
+// as row `row` of the sampler-wide config (seed_base + row).
+static int reseed_row(vdx_sampler *s, int32_t row) {
+  const bool own = s->own_seed[row] != 0;
+  HIP_TRY(s, launch_row_reset(s->d_rows, row, 1, false, -1, true, own ? s->own_seed_val[row] : s->seed_base,
+                              !own, s->stream));
+  return VDX_OK;
+}
+
+// Reseeds rows [0, max_rows): SeedPRNG (Sampler.pas:224-241) with Seed + row,
+// or a row's own Seed.
 static int reseed_all(vdx_sampler *s) {
   s->seed_base = (s->cfg.seed == 0) ? timer_seed() : (uint64_t)s->cfg.seed;
-  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, false, true, s->seed_base, s->stream));
+  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, false, -1, true, s->seed_base, true, s->stream));
+  for (int32_t r = 0; r < s->max_rows; ++r)
+    if (s->own_seed[r]) {
+      int rc = reseed_row(s, r);
+      if (rc != VDX_OK) return rc;
+    }
   HIP_TRY(s, hipStreamSynchronize(s->stream));
   return VDX_OK;
 }
 
+static int32_t window_of(const vdx_sampler_config &c) { return c.repeat_window > 0 ? c.repeat_window : 0; }
+
+// Every row gets `window`; the rings are cleared (SetConfig, Sampler.pas:137-142).
 static int alloc_history(vdx_sampler *s, int32_t window) {
   if (s->d_hist) {
     (void)hipFree(s->d_hist);
@@ -99,9 +123,47 @@ static int alloc_history(vdx_sampler *s, int32_t window) {
     HIP_TRY(s, hipMalloc(&s->d_hist, bytes));
     HIP_TRY(s, hipMemsetAsync(s->d_hist, 0, bytes, s->stream));
   }
-  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, true, false, 0, s->stream));
+  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, true, s->hist_len, false, 0, false, s->stream));
   HIP_TRY(s, hipStreamSynchronize(s->stream));
   s->hist_maybe = false;
+  return VDX_OK;
+}
+
+// Widens the ring stride to `stride`, keeping every row's ids in place.
+// The device must be idle.
+static int grow_history(vdx_sampler *s, int32_t stride) {
+  if (stride <= s->hist_len) return VDX_OK;
+  int32_t *nh = nullptr;
+  const size_t bytes = (size_t)s->max_rows * stride * sizeof(int32_t);
+  HIP_TRY(s, hipMalloc(&nh, bytes));
+  HIP_TRY(s, hipMemset(nh, 0, bytes));
+  if (s->d_hist && s->hist_len > 0)
+    HIP_TRY(s, hipMemcpy2D(nh, sizeof(int32_t) * stride, s->d_hist, sizeof(int32_t) * s->hist_len,
+                           sizeof(int32_t) * s->hist_len, s->max_rows, hipMemcpyDeviceToDevice));
+  HIP_TRY(s, hipDeviceSynchronize());
+  (void)hipFree(s->d_hist);
+  s->d_hist = nh;
+  s->hist_len = stride;
+  return VDX_OK;
+}
+
+static RowCfg row_params(const vdx_sampler_config &c) {
+  RowCfg r{};
+  r.greedy = c.temperature == 0.0f;
+  r.inv_t = r.greedy ? 0.0f : 1.0f / c.temperature;  // Sampler.pas:325
+  r.top_k = c.top_k;
+  r.top_p = c.top_p;
+  r.min_p = c.min_p;
+  r.penalty = c.repeat_penalty;
+  r.window = window_of(c);
+  return r;
+}
+
+// Copies every row's parameters to the device (the device is idle).
+static int upload_row_params(vdx_sampler *s) {
+  std::vector<RowCfg> h((size_t)s->max_rows);
+  for (int32_t r = 0; r < s->max_rows; ++r) h[r] = row_params(s->row_cfg[r]);
+  HIP_TRY(s, hipMemcpy(s->d_rcfg, h.data(), sizeof(RowCfg) * h.size(), hipMemcpyHostToDevice));
   return VDX_OK;
 }
 
@@ -157,6 +219,7 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipSetDevice(s->device);
   if (s->stream) (void)hipStreamSynchronize(s->stream);
   (void)hipFree(s->d_rows);
+  (void)hipFree(s->d_rcfg);
   (void)hipFree(s->d_hist);
   (void)hipFree(s->d_meta);
   (void)hipFree(s->d_cand);
@@ -190,6 +253,9 @@ int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows) {
   s->device = device;
   s->max_rows = max_rows;
   vdx_sampler_default_config(&s->cfg);
+  s->row_cfg.assign((size_t)max_rows, s->cfg);
+  s->own_seed.assign((size_t)max_rows, 0);
+  s->own_seed_val.assign((size_t)max_rows, 0);
   int rc = VDX_OK;
   do {
     if ((e = hipSetDevice(device)) != hipSuccess) { rc = hip_fail(s, e, "hipSetDevice"); break; }
@@ -203,6 +269,10 @@ int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows) {
     }
     if ((e = hipMemset(s->d_rows, 0, sizeof(RowState) * max_rows)) != hipSuccess) {
       rc = hip_fail(s, e, "hipMemset(rows)");
+      break;
+    }
+    if ((e = hipMalloc(&s->d_rcfg, sizeof(RowCfg) * max_rows)) != hipSuccess) {
+      rc = hip_fail(s, e, "hipMalloc(row configs)");
       break;
     }
     if ((e = hipMalloc(&s->d_tickets, sizeof(uint32_t) * max_rows)) != hipSuccess) {
@@ -234,19 +304,69 @@ int vdx_sampler_set_config(vdx_sampler *s, const vdx_sampler_config *c) {
   if (!s || !c) return VDX_E_INVALID_ARG;
   HIP_TRY(s, hipSetDevice(s->device));
   const bool seed_changed = c->seed != s->cfg.seed;
-  s->cfg = *c;
-  const int32_t want = c->repeat_window > 0 ? c->repeat_window : 0;
-  if (want != s->hist_len) {
-    int rc = alloc_history(s, c->repeat_window);
-    if (rc != VDX_OK) return rc;
+  const int32_t want = window_of(*c);
+  int rc = VDX_OK;
+  if (!s->per_row) {
+    if (want != s->hist_len && (rc = alloc_history(s, want)) != VDX_OK) return rc;
+  } else {
+    // every row takes the sampler-wide config again: rows whose window
+    // changes lose their history, rows with their own seed are reseeded
+    HIP_TRY(s, hipDeviceSynchronize());
+    if ((rc = grow_history(s, want)) != VDX_OK) return rc;
+    for (int32_t r = 0; r < s->max_rows; ++r)
+      if (window_of(s->row_cfg[r]) != want)
+        HIP_TRY(s, launch_row_reset(s->d_rows, r, 1, true, want, false, 0, false, s->stream));
   }
+  const bool reseed_own = s->per_row && !seed_changed;
+  s->cfg = *c;
+  s->row_cfg.assign((size_t)s->max_rows, *c);
+  s->per_row = false;
+  if (reseed_own) {
+    for (int32_t r = 0; r < s->max_rows; ++r)
+      if (s->own_seed[r]) {
+        s->own_seed[r] = 0;
+        if ((rc = reseed_row(s, r)) != VDX_OK) return rc;
+      }
+    HIP_TRY(s, hipStreamSynchronize(s->stream));
+  }
+  s->own_seed.assign((size_t)s->max_rows, 0);
   if (seed_changed) return reseed_all(s);
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
   return VDX_OK;
 }
 
 int vdx_sampler_get_config(const vdx_sampler *s, vdx_sampler_config *out) {
   if (!s || !out) return VDX_E_INVALID_ARG;
   *out = s->cfg;
+  return VDX_OK;
+}
+
+int vdx_sampler_set_row_config(vdx_sampler *s, int32_t row, const vdx_sampler_config *c) {
+  if (!s || !c || row < 0 || row >= s->max_rows)
+    return fail(s, VDX_E_INVALID_ARG, "set_row_config: need a config and 0 <= row < max_rows");
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, hipDeviceSynchronize());  // no call in flight reads the row's state
+  const vdx_sampler_config old = s->row_cfg[row];
+  s->row_cfg[row] = *c;
+  s->per_row = true;
+  int rc = VDX_OK;
+  const int32_t w = window_of(*c);
+  if (window_of(old) != w) {  // SetConfig: a new window clears the history (Sampler.pas:137-142)
+    if ((rc = grow_history(s, w)) != VDX_OK) return rc;
+    HIP_TRY(s, launch_row_reset(s->d_rows, row, 1, true, w, false, 0, false, s->stream));
+  }
+  if (old.seed != c->seed) {  // a new Seed reseeds the row from it (Sampler.pas:144-150)
+    s->own_seed[row] = 1;
+    s->own_seed_val[row] = c->seed == 0 ? timer_seed() : (uint64_t)c->seed;
+    if ((rc = reseed_row(s, row)) != VDX_OK) return rc;
+  }
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  return upload_row_params(s);
+}
+
+int vdx_sampler_get_row_config(const vdx_sampler *s, int32_t row, vdx_sampler_config *out) {
+  if (!s || !out || row < 0 || row >= s->max_rows) return VDX_E_INVALID_ARG;
+  *out = s->row_cfg[row];
   return VDX_OK;
 }
 
@@ -268,11 +388,31 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   if (vocab <= 0 || row_stride < vocab)
     return fail(s, VDX_E_INVALID_ARG, "process_device: need vocab > 0 and row_stride >= vocab");
   const vdx_sampler_config &c = s->cfg;
-  const bool greedy = (c.temperature == 0.0f);
-  const bool topk = !greedy && c.top_k > 0 && c.top_k < vocab;
-  if ((out->topk_idx || out->topk_prob) && topk && out->topk_stride < c.top_k)
+  // the paths this call takes (with per-row configs: any of the rows')
+  bool path_any[3] = {false, false, false};
+  bool pen_fused = false, pen_sep = false, full_minp = false;
+  int32_t kmax = 0;
+  if (!s->per_row) {
+    const RowCfg rc = row_params(c);
+    path_any[row_path(rc, vocab)] = true;
+    kmax = rc.top_k;
+    pen_fused = row_fuses_penalty(rc, vocab);
+    pen_sep = rc.penalty != 1.0f && !pen_fused;
+    full_minp = rc.min_p > 0.0f;
+  } else {
+    for (int32_t r = 0; r < rows; ++r) {
+      const RowCfg rc = row_params(s->row_cfg[r]);
+      const int path = row_path(rc, vocab);
+      path_any[path] = true;
+      if (path == 1 && rc.top_k > kmax) kmax = rc.top_k;
+      if (rc.penalty != 1.0f) (row_fuses_penalty(rc, vocab) ? pen_fused : pen_sep) = true;
+      if (path == 2 && rc.min_p > 0.0f) full_minp = true;
+    }
+  }
+  const bool topk = path_any[1];
+  if ((out->topk_idx || out->topk_prob) && topk && out->topk_stride < kmax)
     return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= TopK");
-  if (topk && c.top_k > kKMax)
+  if (topk && kmax > kKMax)
     return fail(s, VDX_E_UNSUPPORTED, "process_device: TopK > 64 is not implemented on the GPU");
   if (chunks_for(vocab) > kMaxChunks)
     return fail(s, VDX_E_UNSUPPORTED, "process_device: vocab > 4194304 is not supported");
@@ -288,17 +428,18 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.vocab = vocab;
   p.nchunks = chunks_for(vocab);
   p.vec = ((uintptr_t)logits % 16 == 0) && (row_stride % 4 == 0) && (vocab % 4 == 0);
-  p.inv_t = greedy ? 0.0f : 1.0f / c.temperature;  // Sampler.pas:325
+  const RowCfg cp = row_params(c);
+  p.inv_t = cp.inv_t;
   p.top_k = c.top_k;
   p.top_p = c.top_p;
-  p.min_p = c.min_p;
+  p.min_p = full_minp ? (s->per_row ? 1.0f : c.min_p) : 0.0f;  // per-row: selects the exact full path
   p.penalty = c.repeat_penalty;
   p.hist = s->d_hist;
   p.hist_len = s->hist_len;
+  p.rcfg = s->per_row ? s->d_rcfg : nullptr;
   p.rng.uniforms = uniforms;
   p.rng.rows = s->d_rows;
   p.rng.kind = s->rng_kind;
-  p.rng.key = s->seed_base;
   p.rng.u_out = out->uniforms;
   p.out.tokens = out->tokens;
   p.out.topk_idx = topk ? out->topk_idx : nullptr;
@@ -312,21 +453,18 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.tickets = s->d_tickets;
 
   // Step 0: repetition penalty (Sampler.pas:287); the top-K kernel applies
-  // it itself for windows of up to kPenMax ids and penalties > 1 (which
-  // never raise a logit); otherwise a separate kernel runs first
-  const bool pen = c.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0;
-  p.fuse_penalty = (pen && topk && s->hist_len <= kPenMax) ? 1 : 0;
+  // it itself for windows of up to kPenMax ids; otherwise a separate kernel
+  // runs first (for the rows that need it)
+  const bool hist = s->hist_maybe && s->hist_len > 0;
+  p.fuse_penalty = (hist && pen_fused) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
-  if (pen && !p.fuse_penalty) HIP_TRY(s, launch_penalty(p, st));
+  if (hist && pen_sep) HIP_TRY(s, launch_penalty(p, st));
   if (timed) HIP_TRY(s, hipEventRecord(ev[1], st));
-  if (greedy)
-    HIP_TRY(s, launch_greedy(p, st));
-  else if (topk)
-    HIP_TRY(s, launch_topk(p, st));
-  else
-    HIP_TRY(s, launch_full(p, st));
+  if (path_any[0]) HIP_TRY(s, launch_greedy(p, st));
+  if (path_any[1]) HIP_TRY(s, launch_topk(p, st));
+  if (path_any[2]) HIP_TRY(s, launch_full(p, st));
   if (timed) {
     HIP_TRY(s, hipEventRecord(ev[2], st));
     ++s->n_timed;
@@ -385,7 +523,7 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
   int32_t tok = -1;
   HIP_TRY(s, hipMemcpyAsync(&tok, s->d_tok, sizeof(int32_t), hipMemcpyDeviceToHost, s->stream));
   // The reference penalises the caller's buffer in place (Sampler.pas:285-303).
-  if (s->cfg.repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
+  if (s->row_cfg[0].repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
     HIP_TRY(s, hipMemcpyAsync(logits, s->d_row, sizeof(float) * (size_t)vocab,
                               hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(s, hipStreamSynchronize(s->stream));
@@ -501,7 +639,7 @@ int vdx_sampler_lmhead_q4_0_device(vdx_sampler *s, const void *weights, const fl
 
 int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token) {
   if (!s || row < 0 || row >= s->max_rows) return VDX_E_INVALID_ARG;
-  if (s->cfg.repeat_window <= 0 || s->hist_len <= 0) return VDX_OK;  // Sampler.pas:532-533
+  if (window_of(s->row_cfg[row]) <= 0 || s->hist_len <= 0) return VDX_OK;  // Sampler.pas:532-533
   HIP_TRY(s, hipSetDevice(s->device));
   HIP_TRY(s, launch_hist_add(nullptr, token, row, 1, s->d_hist, s->hist_len, s->d_rows, s->stream));
   HIP_TRY(s, hipStreamSynchronize(s->stream));
@@ -512,7 +650,7 @@ int vdx_sampler_add_to_history(vdx_sampler *s, int32_t row, int32_t token) {
 int vdx_sampler_add_to_history_device(vdx_sampler *s, const int32_t *tokens, int32_t rows,
                                       void *stream) {
   if (!s || !tokens || rows <= 0 || rows > s->max_rows) return VDX_E_INVALID_ARG;
-  if (s->cfg.repeat_window <= 0 || s->hist_len <= 0) return VDX_OK;
+  if (s->hist_len <= 0) return VDX_OK;  // rows with no window are skipped by the kernel
   HIP_TRY(s, hipSetDevice(s->device));
   HIP_TRY(s, launch_hist_add(tokens, 0, 0, rows, s->d_hist, s->hist_len, s->d_rows,
                              (hipStream_t)stream));
@@ -526,8 +664,17 @@ int vdx_sampler_reset_history(vdx_sampler *s, int32_t row) {
   const int32_t r0 = row < 0 ? 0 : row;
   const int32_t n = row < 0 ? s->max_rows : 1;
   // ResetHistory (Sampler.pas:541-549): reseed only when Seed > 0
-  const bool reseed = s->cfg.seed > 0;
-  HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, reseed, s->seed_base, s->stream));
+  if (!s->per_row) {
+    const bool reseed = s->cfg.seed > 0;
+    HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, -1, reseed, s->seed_base, true, s->stream));
+  } else {
+    HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, -1, false, 0, false, s->stream));
+    for (int32_t r = r0; r < r0 + n; ++r)
+      if (s->row_cfg[r].seed > 0) {
+        int rc = reseed_row(s, r);
+        if (rc != VDX_OK) return rc;
+      }
+  }
   HIP_TRY(s, hipStreamSynchronize(s->stream));
   if (row < 0) s->hist_maybe = false;
   return VDX_OK;
@@ -535,9 +682,9 @@ int vdx_sampler_reset_history(vdx_sampler *s, int32_t row) {
 
 int vdx_sampler_set_history(vdx_sampler *s, int32_t row, const int32_t *ids, int32_t count,
                             int32_t pos) {
-  if (!s || row < 0 || row >= s->max_rows || count < 0 || count > s->hist_len ||
-      (count > 0 && !ids) || pos < 0 || (s->hist_len > 0 && pos >= s->hist_len) ||
-      (s->hist_len == 0 && pos != 0))
+  if (!s || row < 0 || row >= s->max_rows) return VDX_E_INVALID_ARG;
+  const int32_t w = window_of(s->row_cfg[row]);
+  if (count < 0 || count > w || (count > 0 && !ids) || pos < 0 || (w > 0 && pos >= w) || (w == 0 && pos != 0))
     return fail(s, VDX_E_INVALID_ARG, "set_history: need 0 <= count <= window, 0 <= pos < window");
   HIP_TRY(s, hipSetDevice(s->device));
   HIP_TRY(s, hipStreamSynchronize(s->stream));
@@ -567,6 +714,74 @@ int32_t vdx_sampler_get_history(vdx_sampler *s, int32_t row, int32_t *ids, int32
                          hipMemcpyDeviceToHost));
   if (pos) *pos = rs.hist_pos;
   return rs.hist_count;
+}
+
+// ---- row checkpoints ---------------------------------------------------------
+// Blob layout (little endian): RowCkpt, then `window` int32 ring slots.
+struct RowCkpt {
+  char magic[4];            // "VDXR"
+  uint32_t version;         // 1
+  vdx_sampler_config cfg;   // the row's config
+  int32_t rng_kind;
+  int32_t own_seed;         // seeded from its own Seed (else as row r of the sampler-wide Seed + r)
+  uint64_t own_seed_val;    // the xoshiro seed of the row's stream (resolved)
+  RowState state;           // RNG words, Philox counter and key, ring position / fill / window
+};
+static_assert(sizeof(RowCkpt) == 120, "checkpoint header layout");
+
+int64_t vdx_sampler_save_row_state(vdx_sampler *s, int32_t row, void *buf, int64_t cap) {
+  if (!s || row < 0 || row >= s->max_rows || cap < 0) return VDX_E_INVALID_ARG;
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, hipDeviceSynchronize());  // the calls issued so far have updated the row
+  RowCkpt h{};
+  memcpy(h.magic, "VDXR", 4);
+  h.version = 1;
+  h.cfg = s->row_cfg[row];
+  h.rng_kind = s->rng_kind;
+  h.own_seed = s->own_seed[row];
+  h.own_seed_val = s->own_seed[row] ? s->own_seed_val[row] : s->seed_base + (uint64_t)row;
+  HIP_TRY(s, hipMemcpy(&h.state, s->d_rows + row, sizeof(RowState), hipMemcpyDeviceToHost));
+  const int32_t w = h.state.window > 0 ? (h.state.window < s->hist_len ? h.state.window : s->hist_len) : 0;
+  h.state.window = w;
+  const int64_t need = (int64_t)sizeof(RowCkpt) + (int64_t)w * (int64_t)sizeof(int32_t);
+  if (!buf || cap < need) return need;
+  memcpy(buf, &h, sizeof(h));
+  if (w > 0)
+    HIP_TRY(s, hipMemcpy((char *)buf + sizeof(h), s->d_hist + (int64_t)row * s->hist_len,
+                         sizeof(int32_t) * (size_t)w, hipMemcpyDeviceToHost));
+  return need;
+}
+
+int vdx_sampler_load_row_state(vdx_sampler *s, int32_t row, const void *buf, int64_t size) {
+  if (!s || row < 0 || row >= s->max_rows || !buf || size < (int64_t)sizeof(RowCkpt))
+    return fail(s, VDX_E_INVALID_ARG, "load_row_state: need a blob and 0 <= row < max_rows");
+  RowCkpt h;
+  memcpy(&h, buf, sizeof(h));
+  if (memcmp(h.magic, "VDXR", 4) != 0 || h.version != 1)
+    return fail(s, VDX_E_INVALID_ARG, "load_row_state: not a row checkpoint (magic / version)");
+  const int32_t w = h.state.window;
+  if (w < 0 || w != window_of(h.cfg) || size != (int64_t)sizeof(RowCkpt) + (int64_t)w * 4 ||
+      h.state.hist_count < 0 || h.state.hist_count > w || h.state.hist_pos < 0 ||
+      (w > 0 ? h.state.hist_pos >= w : h.state.hist_pos != 0))
+    return fail(s, VDX_E_INVALID_ARG, "load_row_state: inconsistent checkpoint");
+  if (h.rng_kind != s->rng_kind)
+    return fail(s, VDX_E_INVALID_ARG, "load_row_state: the checkpoint was taken with another RNG kind");
+  HIP_TRY(s, hipSetDevice(s->device));
+  HIP_TRY(s, hipDeviceSynchronize());
+  int rc = grow_history(s, w);
+  if (rc != VDX_OK) return rc;
+  s->row_cfg[row] = h.cfg;
+  s->per_row = true;
+  // the restored state carries its own seed: later reseeds of this row
+  // (ResetHistory with Seed > 0, set_rng) start the stream it was taken from
+  s->own_seed[row] = 1;
+  s->own_seed_val[row] = h.own_seed_val;
+  HIP_TRY(s, hipMemcpy(s->d_rows + row, &h.state, sizeof(RowState), hipMemcpyHostToDevice));
+  if (w > 0)
+    HIP_TRY(s, hipMemcpy(s->d_hist + (int64_t)row * s->hist_len, (const char *)buf + sizeof(h),
+                         sizeof(int32_t) * (size_t)w, hipMemcpyHostToDevice));
+  if (h.state.hist_count > 0) s->hist_maybe = true;
+  return upload_row_params(s);
 }
 
 }  // extern "C"

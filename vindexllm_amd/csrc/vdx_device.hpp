@@ -26,9 +26,38 @@ constexpr int kPenMax = 256;                   // history ids handled inside the
 struct RowState {
   uint64_t rng[4];      // xoshiro256** state (Sampler.pas:41-45)
   uint64_t step;        // Philox block counter
+  uint64_t key;         // Philox key (the resolved seed)
   int32_t hist_pos;     // ring write position (Sampler.pas:49)
   int32_t hist_count;   // ring fill (Sampler.pas:50)
+  int32_t window;       // ring length, RepeatWindow (Sampler.pas:47); <= 0: no history
+  int32_t ctr_row;      // Philox counter word 1: the row the stream was seeded on
 };
+static_assert(sizeof(RowState) == 64, "RowState is 64 bytes");
+
+// Per-row sampling parameters, when rows of one sampler carry their own
+// configs: the values of a TVdxSamplerConfig (Sampler.pas:26-34) as the
+// kernels use them.
+struct RowCfg {
+  float inv_t;          // fl32(1 / T) (Sampler.pas:325); 0 when T = 0
+  int32_t top_k;
+  float top_p;
+  float min_p;
+  float penalty;
+  int32_t window;
+  int32_t greedy;       // T = 0 (Sampler.pas:305)
+  int32_t pad;
+};
+
+// Sampling path of a row over V logits (Sampler.pas:305, 327, 461):
+// 0 greedy, 1 top-K, 2 full softmax.
+__host__ __device__ __forceinline__ int row_path(const RowCfg &c, int V) {
+  return c.greedy ? 0 : ((c.top_k > 0 && c.top_k < V) ? 1 : 2);
+}
+// The top-K kernel applies this row's penalty itself (its window fits the
+// kernel's history table); other penalised rows take the separate kernel.
+__host__ __device__ __forceinline__ bool row_fuses_penalty(const RowCfg &c, int V) {
+  return c.penalty != 1.0f && row_path(c, V) == 1 && c.window <= kPenMax;
+}
 
 // Top-K stream phase: one record per (row, chunk):
 //   w    = tau_key | flags << 32  (every logit with key >= tau_key is stored;
@@ -90,8 +119,7 @@ __device__ __forceinline__ float xloadf(const float *p) {
 struct KernelRng {
   const float *uniforms;  // injected per-row u (nullable)
   RowState *rows;
-  int32_t kind;           // 0 xoshiro, 1 philox
-  uint64_t key;           // Philox key word 0 (resolved seed)
+  int32_t kind;           // 0 xoshiro, 1 philox (key: RowState::key)
   float *u_out;           // optional copy of the consumed u
 };
 
@@ -276,6 +304,8 @@ __device__ __forceinline__ float u24(uint64_t x) {
 struct RngPre {
   uint64_t s[4];
   uint64_t step;
+  uint64_t key;
+  uint32_t ctr_row;
   float u;
 };
 __device__ __forceinline__ RngPre rng_prefetch(const KernelRng &g, int row) {
@@ -283,6 +313,8 @@ __device__ __forceinline__ RngPre rng_prefetch(const KernelRng &g, int row) {
   const float *up = g.uniforms ? g.uniforms + row : reinterpret_cast<const float *>(&g.rows[row].step);
   r.u = *up;
   r.step = g.rows[row].step;
+  r.key = g.rows[row].key;
+  r.ctr_row = (uint32_t)g.rows[row].ctr_row;
   r.s[0] = g.rows[row].rng[0];
   r.s[1] = g.rows[row].rng[1];
   r.s[2] = g.rows[row].rng[2];
@@ -296,7 +328,7 @@ __device__ __forceinline__ float rng_draw(const KernelRng &g, int row, RngPre &r
   if (g.uniforms) {
     u = r.u;
   } else if (g.kind == 1) {
-    u = u24(philox4x64_10_w0(r.step, (uint64_t)row, 0, 0, g.key, 0));
+    u = u24(philox4x64_10_w0(r.step, (uint64_t)r.ctr_row, 0, 0, r.key, 0));
     g.rows[row].step = r.step + 1;
   } else {
     u = u24(xoshiro_next(r.s));

@@ -21,9 +21,10 @@ struct CallParams {
   float top_p;
   float min_p;
   float penalty;
-  const int32_t *hist;  // [max_rows * hist_len]
-  int32_t hist_len;
+  const int32_t *hist;  // [max_rows * hist_len]: row r's ring at hist + r * hist_len
+  int32_t hist_len;     // ring stride (>= every row's window)
   int32_t fuse_penalty; // the top-K kernel applies the penalty itself
+  const RowCfg *rcfg;   // per-row parameters (nullptr: the fields above for every row)
   KernelRng rng;
   KernelOut out;
   // workspace
@@ -61,7 +62,7 @@ hipError_t launch_full(const CallParams &p, hipStream_t st);
 hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row0,
                            int32_t rows, int32_t *hist, int32_t hist_len,
                            RowState *rs, hipStream_t st);
-hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist,
-                            bool reseed, uint64_t seed_base, hipStream_t st);
+hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, int32_t window,
+                            bool reseed, uint64_t seed, bool add_row, hipStream_t st);
 
 }  // namespace vdx

@@ -30,6 +30,27 @@ __device__ __forceinline__ f32x4 xload4(const float *p) {
   return r;
 }
 
+// Rows with their own configs (p.rcfg): whether `row` takes path `path` in
+// this launch (the kernels of the other paths skip it), and the call's
+// parameters as the row sees them.  Without per-row configs every row takes
+// the launch's path with the call's parameters.
+__device__ __forceinline__ bool row_on_path(const CallParams &p, int row, int path) {
+  return !p.rcfg || row_path(p.rcfg[row], p.vocab) == path;
+}
+__device__ __forceinline__ CallParams for_row(const CallParams &p, int row) {
+  CallParams q = p;
+  if (p.rcfg) {
+    const RowCfg c = p.rcfg[row];
+    q.inv_t = c.inv_t;
+    q.top_k = c.top_k;
+    q.top_p = c.top_p;
+    q.min_p = c.min_p;
+    q.penalty = c.penalty;
+    q.fuse_penalty = (p.fuse_penalty && row_fuses_penalty(c, p.vocab)) ? 1 : 0;
+  }
+  return q;
+}
+
 // Block-wide exclusive scan of one double per thread (kBlock threads).
 __device__ __forceinline__ double block_excl_scan_f64(double x, double *wtot, double &total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -158,16 +179,19 @@ __device__ __forceinline__ float penalise_fast(float x, int k, float pen, double
   return x;
 }
 
-__global__ __launch_bounds__(kBlock) void k_penalty(float *__restrict__ logits, int64_t stride,
-                                                    int32_t V, const int32_t *__restrict__ hist,
-                                                    int32_t W, const RowState *__restrict__ rs,
-                                                    float pen) {
+// With per-row configs, a row runs here when its penalty is not 1 and the
+// top-K kernel does not apply it.
+__global__ __launch_bounds__(kBlock) void k_penalty(CallParams p0) {
   __shared__ __align__(16) int32_t sh[kPenStage];
   const int row = blockIdx.x;
-  const int cnt = min(rs[row].hist_count, W);
+  const CallParams p = for_row(p0, row);
+  if (p.penalty == 1.0f || p.fuse_penalty) return;
+  const int V = p.vocab, W = p.hist_len;
+  const float pen = p.penalty;
+  const int cnt = min(p.rng.rows[row].hist_count, W);
   if (cnt <= 0) return;
-  const int32_t *h = hist + (int64_t)row * W;
-  float *L = logits + (int64_t)row * stride;
+  const int32_t *h = p.hist + (int64_t)row * W;
+  float *L = p.logits + (int64_t)row * p.stride;
   if (cnt > kPenStage) {
     // long windows: the same rule with the ids read from HBM
     for (int j = threadIdx.x; j < cnt; j += kBlock) {
@@ -218,6 +242,7 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
   __shared__ int s_last;
   int row, chunk;
   block_row_chunk(p.nchunks, p.rows, row, chunk);
+  if (!row_on_path(p, row, 0)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const float *L = p.logits + (int64_t)row * p.stride;
   const int c0 = chunk * kChunk;
@@ -1625,10 +1650,12 @@ __device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSm
 }
 
 template <bool VEC>
-__device__ __forceinline__ void topk_body(const CallParams &p) {
+__device__ __forceinline__ void topk_body(const CallParams &p0) {
   __shared__ TopkSmem sm;
   int row, chunk;
-  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  block_row_chunk(p0.nchunks, p0.rows, row, chunk);
+  if (!row_on_path(p0, row, 1)) return;
+  const CallParams p = for_row(p0, row);
   const int S = p.nchunks, K = p.top_k;
   const float *L = p.logits + (int64_t)row * p.stride;
   const int c0 = chunk * kChunk;
@@ -1702,11 +1729,13 @@ struct FullSmem {
 };
 
 template <bool VEC>
-__global__ __launch_bounds__(kBlock) void k_full_max(CallParams p) {
+__global__ __launch_bounds__(kBlock) void k_full_max(CallParams p0) {
   __shared__ float s_m[kWaves];
   __shared__ uint32_t s_f[kWaves];
   int row, chunk;
-  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  block_row_chunk(p0.nchunks, p0.rows, row, chunk);
+  if (!row_on_path(p0, row, 2)) return;
+  const CallParams p = for_row(p0, row);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const float *L = p.logits + (int64_t)row * p.stride;
   const int c0 = chunk * kChunk;
@@ -1739,10 +1768,12 @@ __global__ __launch_bounds__(kBlock) void k_full_max(CallParams p) {
 }
 
 template <bool VEC, bool EXACT>
-__global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
+__global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   __shared__ FullSmem sm;
   int row, chunk;
-  block_row_chunk(p.nchunks, p.rows, row, chunk);
+  block_row_chunk(p0.nchunks, p0.rows, row, chunk);
+  if (!row_on_path(p0, row, 2)) return;
+  const CallParams p = for_row(p0, row);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int S = p.nchunks, V = p.vocab;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -1954,15 +1985,19 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p) {
 // =============================================================================
 // History ring (Sampler.pas:530-549) and RNG seeding (Sampler.pas:194-241).
 // =============================================================================
+// AddToHistory (Sampler.pas:530-539) for rows [row0, row0 + rows): the ring of
+// row r holds its own window's ids at hist + r * stride.
 __global__ void k_hist_add(const int32_t *__restrict__ tokens, int32_t tok_const, int32_t row0,
-                           int32_t rows, int32_t *__restrict__ hist, int32_t W,
+                           int32_t rows, int32_t *__restrict__ hist, int32_t stride,
                            RowState *__restrict__ rs) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows || W <= 0) return;
+  if (r >= rows) return;
   const int row = row0 + r;
-  const int32_t tok = tokens ? tokens[r] : tok_const;
   RowState &s = rs[row];
-  hist[(int64_t)row * W + s.hist_pos] = tok;
+  const int W = min(s.window, stride);
+  if (W <= 0) return;
+  const int32_t tok = tokens ? tokens[r] : tok_const;
+  hist[(int64_t)row * stride + s.hist_pos] = tok;
   s.hist_pos = (s.hist_pos + 1) % W;
   if (s.hist_count < W) s.hist_count = s.hist_count + 1;
 }
@@ -1975,8 +2010,13 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t &s) {
   return z ^ (z >> 31);
 }
 
+// Clears the rings of rows [row0, row0 + rows) (and sets their window when
+// window >= 0) and/or reseeds them (SeedPRNG, Sampler.pas:224-241): with
+// seed + row (rows of the sampler-wide config behave as samplers with Seed +
+// r), or with `seed` itself (a row with its own config).  The Philox stream
+// of a row is keyed by `seed` and counts on (step, row).
 __global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t rows, int clear_hist,
-                            int reseed, uint64_t seed_base) {
+                            int32_t window, int reseed, uint64_t seed, int add_row) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   const int row = row0 + r;
@@ -1984,9 +2024,12 @@ __global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t row
   if (clear_hist) {
     s.hist_pos = 0;
     s.hist_count = 0;
+    if (window >= 0) s.window = window;
   }
   if (reseed) {
-    uint64_t st = seed_base + (uint64_t)row;  // row r behaves as a sampler with Seed + r
+    uint64_t st = seed + (add_row ? (uint64_t)row : 0ull);
+    s.key = seed;
+    s.ctr_row = row;
     s.rng[0] = splitmix64(st);
     s.rng[1] = splitmix64(st);
     s.rng[2] = splitmix64(st);
@@ -2003,8 +2046,7 @@ static inline dim3 grid_rows_chunks(const CallParams &p) {
 }
 
 hipError_t launch_penalty(const CallParams &p, hipStream_t st) {
-  hipLaunchKernelGGL(k_penalty, dim3(p.rows), dim3(kBlock), 0, st, p.logits, p.stride, p.vocab,
-                     p.hist, p.hist_len, (const RowState *)p.rng.rows, p.penalty);
+  hipLaunchKernelGGL(k_penalty, dim3(p.rows), dim3(kBlock), 0, st, p);
   return hipGetLastError();
 }
 
@@ -2051,11 +2093,11 @@ hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row
   return hipGetLastError();
 }
 
-hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, bool reseed,
-                            uint64_t seed_base, hipStream_t st) {
+hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, int32_t window,
+                            bool reseed, uint64_t seed, bool add_row, hipStream_t st) {
   const int nb = (rows + 255) / 256;
   hipLaunchKernelGGL(k_row_reset, dim3(nb), dim3(256), 0, st, rs, row0, rows, clear_hist ? 1 : 0,
-                     reseed ? 1 : 0, seed_base);
+                     window, reseed ? 1 : 0, seed, add_row ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -106,6 +106,10 @@ _SIGNATURES = {
     "vdx_sampler_destroy": (None, [C.c_void_p]),
     "vdx_sampler_set_config": (C.c_int, [C.c_void_p, C.POINTER(TVdxSamplerConfig)]),
     "vdx_sampler_get_config": (C.c_int, [C.c_void_p, C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_set_row_config": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_get_row_config": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(TVdxSamplerConfig)]),
+    "vdx_sampler_save_row_state": (C.c_int64, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64]),
+    "vdx_sampler_load_row_state": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64]),
     "vdx_sampler_process": (C.c_int32, [C.c_void_p, C.POINTER(C.c_float), C.c_int32]),
     "vdx_sampler_process_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                              C.c_int64, C.c_void_p, C.POINTER(_Outputs),
@@ -241,6 +245,38 @@ class TVdxSampler:
     def SetRng(self, kind: int):
         self._check(load_library().vdx_sampler_set_rng(self._h, int(kind)))
 
+    # -- per-row configs and checkpoints (beyond the reference) -------------
+    def SetRowConfig(self, row: int, cfg: TVdxSamplerConfig):
+        """SetConfig for one row of the batch (SetConfig's rules applied to
+        that row; a changed Seed reseeds the row from Seed itself, so the row
+        draws what a reference sampler with ``cfg`` draws)."""
+        self._check(load_library().vdx_sampler_set_row_config(self._h, int(row), C.byref(cfg)))
+
+    def GetRowConfig(self, row: int) -> TVdxSamplerConfig:
+        c = TVdxSamplerConfig()
+        self._check(load_library().vdx_sampler_get_row_config(self._h, int(row), C.byref(c)))
+        return c
+
+    def save_row_state(self, row: int) -> bytes:
+        """The row's sampler state (config, RNG state, history ring) as bytes."""
+        L = load_library()
+        n = self._check(L.vdx_sampler_save_row_state(self._h, int(row), None, 0))
+        buf = C.create_string_buffer(n)
+        self._check(L.vdx_sampler_save_row_state(self._h, int(row), buf, n))
+        return buf.raw
+
+    def load_row_state(self, row: int, blob: bytes):
+        b = bytes(blob)
+        self._check(load_library().vdx_sampler_load_row_state(self._h, int(row), b, len(b)))
+
+    def save_state(self):
+        """Every row's state (a list of blobs, row order)."""
+        return [self.save_row_state(r) for r in range(self.max_rows)]
+
+    def load_state(self, blobs):
+        for r, b in enumerate(blobs):
+            self.load_row_state(r, b)
+
     # -- sampling -------------------------------------------------------------
     def Process(self, logits, vocab_size: int | None = None) -> int:
         """Process (Sampler.pas:265-528) on a host float32 numpy array, which is
@@ -371,14 +407,14 @@ class TVdxSampler:
 
         a = np.ascontiguousarray(ids, dtype=np.int32)
         n = int(a.size)
-        p = (n % max(self.GetConfig().RepeatWindow, 1)) if pos is None else int(pos)
+        p = (n % max(self.GetRowConfig(row).RepeatWindow, 1)) if pos is None else int(pos)
         self._check(load_library().vdx_sampler_set_history(
             self._h, int(row), a.ctypes.data_as(C.POINTER(C.c_int32)) if n else None, n, p))
 
     def get_history(self, row: int = 0):
         import numpy as np
 
-        cap = max(self.GetConfig().RepeatWindow, 0)
+        cap = max(self.GetRowConfig(row).RepeatWindow, 0)
         buf = np.zeros(max(cap, 1), dtype=np.int32)
         pos = C.c_int32()
         n = self._check(load_library().vdx_sampler_get_history(
