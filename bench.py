@@ -66,10 +66,21 @@ WORKLOADS = {
     "single_row": dict(
         rows=1, vocab=262144, hist=0, cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3001),
         desc="B=1 V=262144 fp32 3*N(0,1)+8 at 16 ids, T 1.0, top-k 64, top-p 0.95"),
+    "mixed_rows_b64": dict(
+        rows=64, vocab=262144, hist=256,
+        cfg=dict(Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256, Seed=3007),
+        row_cfgs=[dict(Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256, Seed=3007),
+                  dict(Temperature=0.0, RepeatPenalty=1.2, RepeatWindow=64, Seed=3008),
+                  dict(Temperature=0.7, TopK=40, TopP=0.9, MinP=0.05, RepeatPenalty=1.3,
+                       RepeatWindow=128, Seed=3009),
+                  dict(Temperature=1.0, TopK=0, RepeatPenalty=1.1, RepeatWindow=256, Seed=3010)],
+        desc="per-row configs: B=64 V=262144 as the penalised batch, rows cycling over "
+             "top-k 64/top-p 0.95 (RP 1.1), greedy (RP 1.2), top-k 40/top-p 0.9/min-p 0.05 "
+             "(RP 1.3) and full softmax T 1.0 (RP 1.1, separate penalty kernel)"),
 }
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
-                   "single_row": "k_topk_vec"}
+                   "single_row": "k_topk_vec", "mixed_rows_b64": "k_topk_vec"}
 
 
 def make_inputs(name, seed=1000):
@@ -84,7 +95,7 @@ def make_inputs(name, seed=1000):
             L[r] = (-1.1 * lr[rng.permutation(V)] + 0.5 * rng.standard_normal(V)).astype(np.float32)
         return L, hist
     L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
-    if name == "penalised_b64":
+    if name in ("penalised_b64", "mixed_rows_b64"):
         hist = np.zeros((B, w["hist"]), dtype=np.int32)
         for r in range(B):
             hot = rng.choice(V, 32, replace=False)
@@ -106,6 +117,12 @@ def configure(s, w):
     for k, v in w["cfg"].items():
         setattr(c, k, v)
     s.SetConfig(c)
+    rc = w.get("row_cfgs")
+    for r in range(w["rows"] if rc else 0):
+        c = s.DefaultConfig()
+        for k, v in rc[r % len(rc)].items():
+            setattr(c, k, v)
+        s.SetRowConfig(r, c)
 
 
 def cpu_baseline(name, L, hist, seconds):
@@ -152,7 +169,7 @@ def run_gpu(name, steps, warmup, eager):
     configure(s, w)
     if hist is not None:
         for r in range(B):
-            s.set_history(r, hist[r])
+            s.set_history(r, hist[r][:max(s.GetRowConfig(r).RepeatWindow, 0)])
     stream = torch.cuda.current_stream(dev)
     for i in range(max(warmup, 1)):
         s.process_device(pool[i % P], tokens=tok, stream=stream)

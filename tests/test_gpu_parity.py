@@ -255,6 +255,29 @@ def test_fused_penalty_paths():
                      label=f"fused penalty V={V} p={p} K={k} P={tp}")
 
 
+def test_fused_penalty_greedy_and_full():
+    # windows of <= 256 ids are applied inside the greedy kernel, the full
+    # kernel, and (with Min-P) the full path's max pass, in place; logits,
+    # tokens and (full path) draws equal the reference's
+    rng = np.random.default_rng(47)
+    for V in (20000, 262144):
+        B = 5
+        L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+        hot = rng.choice(V, 8, replace=False)
+        L[:, hot] += np.float32(7.0)
+        L[0, 5] = 0.0
+        hist = rng.integers(-5, V + 5, (B, 200)).astype(np.int32)
+        hist[:, :60] = rng.choice(hot, (B, 60))
+        hist[:, 60:80] = 5
+        hist[1, :] = hot[0]
+        hist[2, 100:140] = V - 1
+        u = u_stream(rng, B)
+        for p in (1.1, 3.0, 0.8, -2.0):
+            for kw in (dict(temperature=0.0), dict(temperature=1.0), dict(temperature=0.7, min_p=0.05)):
+                _run(L, dict(kw, repeat_penalty=p, repeat_window=200), u, hist=hist,
+                     label=f"fused penalty V={V} p={p} {kw}")
+
+
 # ------------------------------------------------------ stateful sampler ----
 def _cfg(s, **kw):
     c = s.DefaultConfig()

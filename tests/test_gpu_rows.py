@@ -16,7 +16,7 @@ from oracle import vdx_oracle as O
 pytestmark = pytest.mark.gpu
 
 # one config per row: every path, the fused (window <= 256) and the separate
-# penalty, Min-P on both selecting paths, Top-P = 1 (replay), K >= V
+# penalty on each, Min-P on both selecting paths, Top-P = 1 (replay), K >= V
 ROWS = [
     dict(temperature=0.0),
     dict(temperature=1.0, top_k=64, top_p=0.95),
@@ -30,7 +30,10 @@ ROWS = [
     dict(temperature=1.1, repeat_penalty=1.5, repeat_window=128),
     dict(temperature=1.0, top_k=64, top_p=1.0),
     dict(temperature=1.0, top_k=3, top_p=0.5, repeat_penalty=3.0, repeat_window=256),
+    dict(temperature=0.9, min_p=0.02, repeat_penalty=1.25, repeat_window=200),
+    dict(temperature=0.0, repeat_penalty=1.4, repeat_window=300),
 ]
+PATHS = [0, 1, 1, 2, 2, 2, 1, 1, 0, 2, 1, 1, 2, 0]
 
 
 def _set(s, row, kw):
@@ -93,7 +96,7 @@ def test_mixed_row_configs_match_per_row_reference(V):
         row = L[r].copy()
         t, tr = O.process_row(row, O.make_config(**_okw(kw)), float(u[r]), hist=hist[r], trace=True)
         orc.append((t, tr, row))
-        assert tr.path == [0, 1, 1, 2, 2, 2, 1, 1, 0, 2, 1, 1][r], (r, tr.path)
+        assert tr.path == PATHS[r], (r, tr.path)
     nb = compare(g, orc, {}, label=f"mixed rows V={V}")
     log(f"[done] mixed row configs V={V}: near-boundary {nb}/{B}, flags {g['flags'].tolist()}")
 
@@ -235,3 +238,43 @@ def test_load_row_state_rejects_bad_blobs():
         s.load_row_state(1, blob)
         b2 = s.save_row_state(1)  # the same blob, except that the row now owns its seed
         assert b2[:44] == blob[:44] and b2[48:] == blob[48:] and b2[44] == 1 and blob[44] == 0
+
+
+def test_mixed_rows_graph_replay_matches_eager():
+    # a mixed-path call (greedy, top-K and full rows run side by side on
+    # forked streams) captured in a hipGraph and replayed with eager work in
+    # between gives the eager result every time
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    log("[case] mixed rows graph replay")
+    rng = np.random.default_rng(74)
+    B, V = len(ROWS), 65536
+    L = (3.0 * rng.standard_normal((B, V))).astype(np.float32)
+    u = torch.from_numpy(u_stream(rng, B)).cuda()
+    pristine = torch.from_numpy(L).cuda()
+    buf = pristine.clone()
+    with TVdxSampler(0, B) as s:
+        for r, kw in enumerate(ROWS):
+            _set(s, r, kw)
+            w = kw.get("repeat_window", 64)
+            s.set_history(r, rng.integers(0, V, w).astype(np.int32))
+        tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+        eager = s.process_device(buf, uniforms=u).clone()
+        eager_logits = buf.clone()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            s.process_device(buf, uniforms=u, tokens=tok, stream=cs)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            buf.copy_(pristine)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(tok, eager), rep
+            assert torch.equal(buf, eager_logits), rep
+            _ = (pristine * 2).sum().item()
+    log("[done] mixed rows graph replay")

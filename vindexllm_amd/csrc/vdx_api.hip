@@ -34,6 +34,11 @@ struct vdx_sampler {
   std::vector<uint8_t> own_seed;            // row seeded from its own Seed (else seed_base + row)
   std::vector<uint64_t> own_seed_val;       // that seed, resolved (timer value for Seed = 0)
   RowCfg *d_rcfg = nullptr;
+  // a call whose rows take several paths runs their kernels side by side:
+  // forked onto these streams after the penalty, joined before returning
+  hipStream_t aux[2] = {nullptr, nullptr};
+  hipEvent_t ev_fork = nullptr;
+  hipEvent_t ev_join[2] = {nullptr, nullptr};
   // workspace (sized for ws_chunks chunks per row)
   int32_t ws_chunks = 0;
   ChunkMeta *d_meta = nullptr;
@@ -147,6 +152,18 @@ static int grow_history(vdx_sampler *s, int32_t stride) {
   return VDX_OK;
 }
 
+// The fork/join streams and events of mixed-path calls (created once, on the
+// first per-row config, never during a call that may be captured).
+static int ensure_aux(vdx_sampler *s) {
+  if (s->aux[0]) return VDX_OK;
+  HIP_TRY(s, hipEventCreateWithFlags(&s->ev_fork, hipEventDisableTiming));
+  for (int i = 0; i < 2; ++i) {
+    HIP_TRY(s, hipStreamCreateWithFlags(&s->aux[i], hipStreamNonBlocking));
+    HIP_TRY(s, hipEventCreateWithFlags(&s->ev_join[i], hipEventDisableTiming));
+  }
+  return VDX_OK;
+}
+
 static RowCfg row_params(const vdx_sampler_config &c) {
   RowCfg r{};
   r.greedy = c.temperature == 0.0f;
@@ -231,6 +248,11 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_xt);
   (void)hipFree(s->d_tok);
   for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
+  if (s->ev_fork) (void)hipEventDestroy(s->ev_fork);
+  for (int i = 0; i < 2; ++i) {
+    if (s->ev_join[i]) (void)hipEventDestroy(s->ev_join[i]);
+    if (s->aux[i]) (void)hipStreamDestroy(s->aux[i]);
+  }
   if (s->stream) (void)hipStreamDestroy(s->stream);
   (void)hipSetDevice(cur);
   delete s;
@@ -346,10 +368,11 @@ int vdx_sampler_set_row_config(vdx_sampler *s, int32_t row, const vdx_sampler_co
     return fail(s, VDX_E_INVALID_ARG, "set_row_config: need a config and 0 <= row < max_rows");
   HIP_TRY(s, hipSetDevice(s->device));
   HIP_TRY(s, hipDeviceSynchronize());  // no call in flight reads the row's state
+  int rc = ensure_aux(s);
+  if (rc != VDX_OK) return rc;
   const vdx_sampler_config old = s->row_cfg[row];
   s->row_cfg[row] = *c;
   s->per_row = true;
-  int rc = VDX_OK;
   const int32_t w = window_of(*c);
   if (window_of(old) != w) {  // SetConfig: a new window clears the history (Sampler.pas:137-142)
     if ((rc = grow_history(s, w)) != VDX_OK) return rc;
@@ -452,9 +475,9 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.gpart = s->d_gpart;
   p.tickets = s->d_tickets;
 
-  // Step 0: repetition penalty (Sampler.pas:287); the top-K kernel applies
-  // it itself for windows of up to kPenMax ids; otherwise a separate kernel
-  // runs first (for the rows that need it)
+  // Step 0: repetition penalty (Sampler.pas:287); the sampling kernels apply
+  // it themselves for windows of up to kPenMax ids; otherwise a separate
+  // kernel runs first (for the rows that need it)
   const bool hist = s->hist_maybe && s->hist_len > 0;
   p.fuse_penalty = (hist && pen_fused) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
@@ -462,9 +485,28 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
   if (hist && pen_sep) HIP_TRY(s, launch_penalty(p, st));
   if (timed) HIP_TRY(s, hipEventRecord(ev[1], st));
-  if (path_any[0]) HIP_TRY(s, launch_greedy(p, st));
-  if (path_any[1]) HIP_TRY(s, launch_topk(p, st));
-  if (path_any[2]) HIP_TRY(s, launch_full(p, st));
+  const int npaths = (int)path_any[0] + (int)path_any[1] + (int)path_any[2];
+  if (npaths == 1 || !s->aux[0]) {
+    if (path_any[0]) HIP_TRY(s, launch_greedy(p, st));
+    if (path_any[1]) HIP_TRY(s, launch_topk(p, st));
+    if (path_any[2]) HIP_TRY(s, launch_full(p, st));
+  } else {
+    // rows of different paths: each path's kernel on its own stream, forked
+    // from the call's stream after the penalty and joined back (the kernels
+    // touch disjoint rows of the logits and of the workspace)
+    HIP_TRY(s, hipEventRecord(s->ev_fork, st));
+    int k = 0;
+    for (int path = 0; path < 3; ++path) {
+      if (!path_any[path] || path == (path_any[1] ? 1 : 2)) continue;  // that one stays on st
+      hipStream_t a = s->aux[k];
+      HIP_TRY(s, hipStreamWaitEvent(a, s->ev_fork, 0));
+      HIP_TRY(s, path == 0 ? launch_greedy(p, a) : launch_full(p, a));
+      HIP_TRY(s, hipEventRecord(s->ev_join[k], a));
+      ++k;
+    }
+    HIP_TRY(s, path_any[1] ? launch_topk(p, st) : launch_full(p, st));
+    for (int i = 0; i < k; ++i) HIP_TRY(s, hipStreamWaitEvent(st, s->ev_join[i], 0));
+  }
   if (timed) {
     HIP_TRY(s, hipEventRecord(ev[2], st));
     ++s->n_timed;
@@ -768,8 +810,9 @@ int vdx_sampler_load_row_state(vdx_sampler *s, int32_t row, const void *buf, int
     return fail(s, VDX_E_INVALID_ARG, "load_row_state: the checkpoint was taken with another RNG kind");
   HIP_TRY(s, hipSetDevice(s->device));
   HIP_TRY(s, hipDeviceSynchronize());
-  int rc = grow_history(s, w);
+  int rc = ensure_aux(s);
   if (rc != VDX_OK) return rc;
+  if ((rc = grow_history(s, w)) != VDX_OK) return rc;
   s->row_cfg[row] = h.cfg;
   s->per_row = true;
   // the restored state carries its own seed: later reseeds of this row

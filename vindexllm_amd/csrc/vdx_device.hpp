@@ -53,10 +53,11 @@ struct RowCfg {
 __host__ __device__ __forceinline__ int row_path(const RowCfg &c, int V) {
   return c.greedy ? 0 : ((c.top_k > 0 && c.top_k < V) ? 1 : 2);
 }
-// The top-K kernel applies this row's penalty itself (its window fits the
-// kernel's history table); other penalised rows take the separate kernel.
+// The sampling kernel applies this row's penalty itself (its window fits the
+// kernels' history table); rows with longer windows take the separate kernel.
 __host__ __device__ __forceinline__ bool row_fuses_penalty(const RowCfg &c, int V) {
-  return c.penalty != 1.0f && row_path(c, V) == 1 && c.window <= kPenMax;
+  (void)V;
+  return c.penalty != 1.0f && c.window <= kPenMax;
 }
 
 // Top-K stream phase: one record per (row, chunk):

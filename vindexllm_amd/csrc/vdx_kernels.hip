@@ -232,65 +232,6 @@ __global__ __launch_bounds__(kBlock) void k_penalty(CallParams p0) {
 }
 
 // =============================================================================
-// Greedy argmax (Sampler.pas:306-322): the reference's strict '>' scan returns
-// the lowest index of the maximum; a NaN at index 0 absorbs the scan (-> 0),
-// NaNs elsewhere are never chosen.  Key = (ordered value << 32) | ~index.
-// =============================================================================
-template <bool VEC>
-__global__ __launch_bounds__(kBlock) void k_greedy(CallParams p) {
-  __shared__ uint64_t s_w[kWaves];
-  __shared__ int s_last;
-  int row, chunk;
-  block_row_chunk(p.nchunks, p.rows, row, chunk);
-  if (!row_on_path(p, row, 0)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const float *L = p.logits + (int64_t)row * p.stride;
-  const int c0 = chunk * kChunk;
-  const int clen = min(kChunk, p.vocab - c0);
-  float v[kPerThread];
-  load_chunk<VEC>(L + c0, clen, wv, lane, v, __builtin_nanf(""));
-  float m = v[0];
-#pragma unroll
-  for (int i = 1; i < kPerThread; ++i) m = fmaxf(m, v[i]);  // NaN-ignoring
-  int first = -1;
-#pragma unroll
-  for (int i = kPerThread - 1; i >= 0; --i)
-    if (v[i] == m) first = i;  // this thread's lowest position of its max
-  uint64_t key = 0;
-  if (first >= 0)
-    key = ((uint64_t)ord_key(m) << 32) |
-          (uint32_t)(~(uint32_t)(c0 + chunk_pos(wv, lane, first)));
-  key = wave_max_u64(key);
-  if (lane == 0) s_w[wv] = key;
-  __syncthreads();
-  if (tid == 0) {
-    uint64_t k = s_w[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
-    xstore(&p.gpart[(int64_t)row * p.nchunks + chunk], k);
-  }
-  if (!last_of_row(p.tickets, row, p.nchunks, &s_last, [] {})) return;
-  uint64_t k = 0;
-  for (int c = tid; c < p.nchunks; c += kBlock) {
-    const uint64_t x = xload(&p.gpart[(int64_t)row * p.nchunks + c]);
-    k = x > k ? x : k;
-  }
-  k = wave_max_u64(k);
-  __syncthreads();
-  if (lane == 0) s_w[wv] = k;
-  __syncthreads();
-  if (tid == 0) {
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
-    int32_t tok = k ? (int32_t)(~(uint32_t)k) : 0;
-    if (L[0] != L[0]) tok = 0;
-    p.out.tokens[row] = tok;
-    if (p.out.flags) p.out.flags[row] = kRowGreedy;
-    if (p.rng.u_out) p.rng.u_out[row] = 0.0f;
-  }
-}
-
-// =============================================================================
 // Top-K path (Sampler.pas:327-460).
 //
 // Stream phase (every 16384-logit chunk): 64 logits per thread in registers;
@@ -416,8 +357,16 @@ __device__ __forceinline__ uint32_t pen_hash(uint32_t id) {
 }
 static_assert(kPenHash == 1024, "pen_hash yields 10 bits");
 
+// The table and bitmap live in each kernel's shared-memory record (SM has
+// members ptab[kPenHash] and pbits[kBlock]).
+struct PenaltySmem {
+  uint32_t ptab[kPenHash];
+  uint64_t pbits[kBlock];  // history positions among each thread's 64 logits
+};
+
 // Empties the table and the position bitmap (before a barrier).
-__device__ __forceinline__ void penalty_clear(TopkSmem &sm) {
+template <class SM>
+__device__ __forceinline__ void penalty_clear(SM &sm) {
 #pragma unroll
   for (int i = 0; i < kPenHash / kBlock; ++i) sm.ptab[threadIdx.x + i * kBlock] = kPenEmpty;
   sm.pbits[threadIdx.x] = 0ull;
@@ -426,9 +375,11 @@ __device__ __forceinline__ void penalty_clear(TopkSmem &sm) {
 // Counts the history ids that fall in chunk [c0, c0 + clen) (at most kPenMax
 // distinct ids in kPenHash slots, so a free slot always exists) and marks
 // their positions: bit 4j + e of sm.pbits[64 wv + lane] is position
-// j*1024 + wv*256 + lane*4 + e (the interleaved chunk layout).
+// chunk_pos<SPAN>(wv, lane, 4j + e), i.e. j*1024 + wv*256 + lane*4 + e in the
+// interleaved layout, wv*4096 + j*256 + lane*4 + e in the wave-span layout.
+template <bool SPAN, class SM>
 __device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, int c0, int clen,
-                                              TopkSmem &sm) {
+                                              SM &sm) {
   const int t = threadIdx.x;
   const int32_t id = pf.id[0];
   if (t < min(pf.cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
@@ -444,19 +395,127 @@ __device__ __forceinline__ void penalty_table(const CallParams &p, const Penalty
       h = (h + 1u) & (uint32_t)(kPenHash - 1);
     }
     const int pos = id - c0;
-    atomicOr(&sm.pbits[((pos >> 8) & 3) * 64 + ((pos >> 2) & 63)],
-             1ull << (((pos >> 10) << 2) | (pos & 3)));
+    if (SPAN)
+      atomicOr(&sm.pbits[(pos >> 12) * 64 + ((pos >> 2) & 63)], 1ull << ((((pos >> 8) & 15) << 2) | (pos & 3)));
+    else
+      atomicOr(&sm.pbits[((pos >> 8) & 3) * 64 + ((pos >> 2) & 63)],
+               1ull << (((pos >> 10) << 2) | (pos & 3)));
   }
 }
 
 // Occurrences of `id` in the history (the id is in the table).
-__device__ __forceinline__ uint32_t pen_count(const TopkSmem &sm, uint32_t id) {
+template <class SM>
+__device__ __forceinline__ uint32_t pen_count(const SM &sm, uint32_t id) {
   uint32_t h = pen_hash(id);
   for (;;) {
     const uint32_t e = sm.ptab[h];
     if (e == kPenEmpty) return 0u;
     if ((e & kPenIdMask) == id) return e >> 22;
     h = (h + 1u) & (uint32_t)(kPenHash - 1);
+  }
+}
+
+// The fused penalty for one chunk whose logits are in flight into v (the
+// table was cleared at kernel start): the history ids of the chunk are
+// counted, then this thread's logits at history positions are penalised in
+// registers and in place (Sampler.pas:285-303).  Everything after runs on
+// penalised values; the stores are acknowledged before the workgroup's ticket.
+template <bool SPAN, class SM>
+__device__ __forceinline__ void penalty_pass(const CallParams &p, int row, int c0, int clen,
+                                             const PenaltyPrefetch &pf, float (&v)[kPerThread], SM &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int kG = kPerThread / 4;
+  __syncthreads();
+  penalty_table<SPAN>(p, pf, c0, clen, sm);
+  __syncthreads();
+  const uint64_t hm = sm.pbits[tid];
+  __builtin_amdgcn_sched_barrier(0);
+  if (__ballot(hm != 0ull)) {
+    float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
+    const double ip = 1.0 / (double)p.penalty;
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      const uint32_t nib = (uint32_t)(hm >> (4 * j)) & 15u;
+      if (__ballot(nib != 0u)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if ((nib >> e) & 1u) {
+            const int idx = c0 + chunk_pos<SPAN>(wv, lane, 4 * j + e);
+            const float x = penalise_fast(v[4 * j + e], (int)pen_count(sm, (uint32_t)idx), p.penalty, ip);
+            v[4 * j + e] = x;
+            xstoref(&Lw[idx], x);
+          }
+        }
+      }
+    }
+  }
+}
+
+// =============================================================================
+// Greedy argmax (Sampler.pas:306-322): the reference's strict '>' scan returns
+// the lowest index of the maximum; a NaN at index 0 absorbs the scan (-> 0),
+// NaNs elsewhere are never chosen.  Key = (ordered value << 32) | ~index.
+// A penalty with a window of up to kPenMax ids is applied here first.
+// =============================================================================
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_greedy(CallParams p0) {
+  __shared__ uint64_t s_w[kWaves];
+  __shared__ int s_last;
+  __shared__ PenaltySmem ps;
+  int row, chunk;
+  block_row_chunk(p0.nchunks, p0.rows, row, chunk);
+  if (!row_on_path(p0, row, 0)) return;
+  const CallParams p = for_row(p0, row);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, p.vocab - c0);
+  PenaltyPrefetch pf;
+  if (p.fuse_penalty) {
+    penalty_prefetch(p, row, pf);
+    penalty_clear(ps);
+  }
+  float v[kPerThread];
+  load_chunk<VEC>(L + c0, clen, wv, lane, v, __builtin_nanf(""));
+  if (p.fuse_penalty) penalty_pass<false>(p, row, c0, clen, pf, v, ps);
+  float m = v[0];
+#pragma unroll
+  for (int i = 1; i < kPerThread; ++i) m = fmaxf(m, v[i]);  // NaN-ignoring
+  int first = -1;
+#pragma unroll
+  for (int i = kPerThread - 1; i >= 0; --i)
+    if (v[i] == m) first = i;  // this thread's lowest position of its max
+  uint64_t key = 0;
+  if (first >= 0)
+    key = ((uint64_t)ord_key(m) << 32) |
+          (uint32_t)(~(uint32_t)(c0 + chunk_pos(wv, lane, first)));
+  key = wave_max_u64(key);
+  if (lane == 0) s_w[wv] = key;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t k = s_w[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
+    xstore(&p.gpart[(int64_t)row * p.nchunks + chunk], k);
+  }
+  if (!last_of_row(p.tickets, row, p.nchunks, &s_last, [] {})) return;
+  uint64_t k = 0;
+  for (int c = tid; c < p.nchunks; c += kBlock) {
+    const uint64_t x = xload(&p.gpart[(int64_t)row * p.nchunks + c]);
+    k = x > k ? x : k;
+  }
+  k = wave_max_u64(k);
+  __syncthreads();
+  if (lane == 0) s_w[wv] = k;
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) k = s_w[w] > k ? s_w[w] : k;
+    int32_t tok = k ? (int32_t)(~(uint32_t)k) : 0;
+    if (L[0] != L[0]) tok = 0;
+    p.out.tokens[row] = tok;
+    if (p.out.flags) p.out.flags[row] = kRowGreedy;
+    if (p.rng.u_out) p.rng.u_out[row] = 0.0f;
   }
 }
 
@@ -467,37 +526,9 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
                                             TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
-  const bool pen = p.fuse_penalty != 0;
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
-  if (pen) {  // while the chunk is in flight (the table was cleared at kernel start)
-    __syncthreads();
-    penalty_table(p, pf, c0, clen, sm);
-    __syncthreads();
-    const uint64_t hm = sm.pbits[tid];
-    __builtin_amdgcn_sched_barrier(0);
-    // the penalised logits at this thread's history positions, in registers
-    // and in place
-    if (__ballot(hm != 0ull)) {
-      float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
-      const double ip = 1.0 / (double)p.penalty;
-#pragma unroll
-      for (int j = 0; j < kG; ++j) {
-        const uint32_t nib = (uint32_t)(hm >> (4 * j)) & 15u;
-        if (__ballot(nib != 0u)) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if ((nib >> e) & 1u) {
-              const int idx = c0 + chunk_pos(wv, lane, 4 * j + e);
-              const float x = penalise_fast(v[4 * j + e], (int)pen_count(sm, (uint32_t)idx), p.penalty, ip);
-              v[4 * j + e] = x;
-              xstoref(&Lw[idx], x);
-            }
-          }
-        }
-      }
-    }
-  }
+  if (p.fuse_penalty) penalty_pass<false>(p, row, c0, clen, pf, v, sm);
 
   // group (float4) maxima and the thread maximum; v_maximum3 propagates NaN,
   // so a NaN or +inf anywhere in the thread's logits shows in `m`
@@ -1712,6 +1743,7 @@ __global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_bod
 // the weights are the reference's q with q < MinP zeroed (Qmax = 1).
 // =============================================================================
 struct FullSmem {
+  PenaltySmem pen;
   float wm[kWaves];
   uint32_t wf[kWaves];
   double wd[kWaves];
@@ -1732,6 +1764,7 @@ template <bool VEC>
 __global__ __launch_bounds__(kBlock) void k_full_max(CallParams p0) {
   __shared__ float s_m[kWaves];
   __shared__ uint32_t s_f[kWaves];
+  __shared__ PenaltySmem ps;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
   if (!row_on_path(p0, row, 2)) return;
@@ -1740,8 +1773,16 @@ __global__ __launch_bounds__(kBlock) void k_full_max(CallParams p0) {
   const float *L = p.logits + (int64_t)row * p.stride;
   const int c0 = chunk * kChunk;
   const int clen = min(kChunk, p.vocab - c0);
+  PenaltyPrefetch pf;
+  if (p.fuse_penalty) {
+    penalty_prefetch(p, row, pf);
+    penalty_clear(ps);
+  }
   float v[kPerThread];
   load_chunk<VEC>(L + c0, clen, wv, lane, v, -INFINITY);
+  // the fused penalty of an exact (Min-P) full pass: applied here, in place,
+  // so k_full reads the penalised row
+  if (p.fuse_penalty) penalty_pass<false>(p, row, c0, clen, pf, v, ps);
   float m = -INFINITY;
   bool bad = false;
 #pragma unroll
@@ -1781,8 +1822,16 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   const int c0 = chunk * kChunk;
   const int clen = min(kChunk, V - c0);
   RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
+  // the fused penalty (without Min-P; with it, k_full_max applied it)
+  const bool pen = !EXACT && p.fuse_penalty;
+  PenaltyPrefetch pf;
+  if (pen) {
+    penalty_prefetch(p, row, pf);
+    penalty_clear(sm.pen);
+  }
   float v[kPerThread];
   load_chunk<VEC, true>(L + c0, clen, wv, lane, v, -INFINITY);
+  if (pen) penalty_pass<true>(p, row, c0, clen, pf, v, sm.pen);
 
   // s = fl32(L * invT); positions past the row end weigh nothing
   float m = -INFINITY;
@@ -1941,7 +1990,8 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
     const int e = e0 + i;
     float w = 0.0f;
     if (e < V) {
-      const float s = L[e] * p.inv_t;
+      // penalised values written by the row's other workgroups are read past the caches
+      const float s = (p.fuse_penalty ? xloadf(&L[e]) : L[e]) * p.inv_t;
       if (EXACT) {
         const float q = (float)exp((double)s - (double)M);
         w = (q < p.min_p) ? 0.0f : q;
