@@ -1743,7 +1743,10 @@ __global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_bod
 // the weights are the reference's q with q < MinP zeroed (Qmax = 1).
 // =============================================================================
 struct FullSmem {
-  PenaltySmem pen;
+  union {
+    PenaltySmem pen;          // stream phase: the fused penalty's table
+    float wseg[kWaveSpan];    // last workgroup: the target segment's weights
+  };
   float wm[kWaves];
   uint32_t wf[kWaves];
   double wd[kWaves];
@@ -1753,8 +1756,8 @@ struct FullSmem {
   uint32_t bad;
   float u;
   int32_t cstar;
-  int32_t hit;
-  int32_t lastnz;
+  int32_t whit[kWaves];
+  int32_t wlast[kWaves];
   double scale;
   double base;
   double cincl[kMaxChunks];
@@ -1935,8 +1938,6 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   if (tid < S) sm.cincl[tid] = incl;
   if (tid == 0) {
     sm.cstar = 0x7FFFFFFF;
-    sm.hit = 0x7FFFFFFF;
-    sm.lastnz = -1;
   }
   __syncthreads();
   const double t = (double)sm.u * total;
@@ -1980,27 +1981,52 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
       before = before - tdw[ws_] * scale;
     }
   }
-  // rescan that segment: thread tid owns 16 consecutive logits
+  // rescan that segment: its weights are computed from coalesced loads
+  // (consecutive lanes read consecutive float4s; penalised values written by
+  // the row's other workgroups are read past the caches) into LDS in index
+  // order, then thread tid takes 16 consecutive weights
   const int seg0 = cs * kChunk + ws_ * kWaveSpan;
   const int e0 = seg0 + tid * 16;
+#pragma unroll
+  for (int q = 0; q < kWaveSpan / (4 * kBlock); ++q) {
+    const int o = q * 4 * kBlock + tid * 4;
+    const int e = seg0 + o;
+    float x[4];
+    if (VEC && e < V) {  // 16-byte aligned rows, V % 4 = 0: the float4 lies in the row
+      const f32x4 f = p.fuse_penalty ? xload4(&L[e]) : *reinterpret_cast<const f32x4 *>(&L[e]);
+      x[0] = f[0];
+      x[1] = f[1];
+      x[2] = f[2];
+      x[3] = f[3];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        x[i] = (e + i < V) ? (p.fuse_penalty ? xloadf(&L[e + i]) : L[e + i]) : 0.0f;
+    }
+    f32x4 w4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float w = 0.0f;
+      if (e + i < V) {
+        const float s = x[i] * p.inv_t;
+        if (EXACT) {
+          const float q = (float)exp((double)s - (double)M);
+          w = (q < p.min_p) ? 0.0f : q;
+        } else {
+          w = expf(s - tcm);
+        }
+      }
+      w4[i] = w;
+    }
+    *reinterpret_cast<f32x4 *>(&sm.wseg[o]) = w4;
+  }
+  __syncthreads();
   float w16[16];
   double tsum = 0.0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int e = e0 + i;
-    float w = 0.0f;
-    if (e < V) {
-      // penalised values written by the row's other workgroups are read past the caches
-      const float s = (p.fuse_penalty ? xloadf(&L[e]) : L[e]) * p.inv_t;
-      if (EXACT) {
-        const float q = (float)exp((double)s - (double)M);
-        w = (q < p.min_p) ? 0.0f : q;
-      } else {
-        w = expf(s - tcm);
-      }
-    }
-    w16[i] = w;
-    tsum += (double)w;
+    w16[i] = sm.wseg[tid * 16 + i];
+    tsum += (double)w16[i];
   }
   double segtot;
   const double tb = block_excl_scan_f64(tsum * scale, sm.wtot, segtot);
@@ -2013,16 +2039,30 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
     run = run + w;
     if (hit < 0 && w16[i] > 0.0f && run > t) hit = e0 + i;
   }
-  if (hit >= 0) atomicMin(&sm.hit, hit);
-  if (lastnz >= 0) atomicMax(&sm.lastnz, lastnz);
+  // thread order is index order here: the first hit is the lowest thread's,
+  // the last non-zero weight the highest thread's (per wave by ballot; LDS
+  // atomics with a different value per lane would run a scalar loop per wave)
+  const uint64_t hb = __ballot(hit >= 0), nb = __ballot(lastnz >= 0);
+  const int hv = __shfl(hit, hb ? __ffsll((unsigned long long)hb) - 1 : 0);  // every lane active
+  const int nv = __shfl(lastnz, nb ? 63 - __clzll((long long)nb) : 0);
+  if (lane == 0) {
+    sm.whit[wv] = hb ? hv : 0x7FFFFFFF;
+    sm.wlast[wv] = nb ? nv : -1;
+  }
   __syncthreads();
   if (tid == 0) {
     int32_t tok;
     uint32_t fl2 = kRowFull;
-    if (sm.hit != 0x7FFFFFFF)
-      tok = sm.hit;
-    else if (sm.lastnz >= 0)
-      tok = sm.lastnz;
+    int32_t h = 0x7FFFFFFF, ln = -1;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      h = (h == 0x7FFFFFFF) ? sm.whit[w] : h;
+      ln = (sm.wlast[w] >= 0) ? sm.wlast[w] : ln;
+    }
+    if (h != 0x7FFFFFFF)
+      tok = h;
+    else if (ln >= 0)
+      tok = ln;
     else {
       tok = V - 1;
       fl2 |= kRowFallback;
