@@ -240,17 +240,18 @@ VALU_FP32_PEAK_TFLOPS = 157.3      # MI355X published FP32 vector peak (packed F
 LMHEAD_FORMATS = {"q4_0": (2, 18), "q8_0": (8, 34), "f16": (1, 64)}  # GGML type id, bytes per 32
 
 
-def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False):
+def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True):
     """lm_head + sampling with the logits kept in HBM (RunUnembedding followed
     by Process, Inference.pas:327-339): the lm_head of 262144 x 2560 in `fmt`
     (Q4_0: nibbles uniform 0..15; Q8_0: int8 uniform; fp16 scales
     |N(0, 0.02)|; F16: N(0, 0.05)), optionally after the output RMSNorm, over
-    B hidden rows N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  Times the
-    whole call and the lm_head alone (norm included), each from a captured
-    hipGraph."""
+    B hidden rows N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  With `packed`
+    the weights are first repacked once (lmhead_pack, outside the timed
+    region) and read in that layout.  Times the whole call and the lm_head
+    alone (norm included), each from a captured hipGraph."""
     import torch
 
-    from vindexllm_amd import TVdxSampler, lmhead
+    from vindexllm_amd import VDX_LMHEAD_PACKED, TVdxSampler, lmhead, lmhead_pack
 
     V, D = LMHEAD_V, LMHEAD_D
     wtype, bb = LMHEAD_FORMATS[fmt]
@@ -265,6 +266,10 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False):
         d = (torch.randn(V, nb, device=dev, generator=g) * 0.02).abs().half()
         w[:, :, 0:2] = d.view(torch.uint8).view(V, nb, 2)
     w = w.reshape(-1)
+    if packed:
+        w = lmhead_pack(w, wtype, D, V)
+        wtype = wtype | VDX_LMHEAD_PACKED
+        torch.cuda.synchronize()
     hidden = torch.randn(B, D, device=dev, generator=g)
     nw = (1.0 + 0.1 * torch.randn(D, device=dev, generator=g)) if norm else None
     logits = torch.empty(B, V, dtype=torch.float32, device=dev)
@@ -321,7 +326,7 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False):
            "lmhead_valu_frac": flops / (head_us * 1e-6) / 1e12 / VALU_FP32_PEAK_TFLOPS,
            "bound": "hbm" if B == 1 else "valu",
            "desc": f"{fmt.upper()} lm_head {V}x{D}{' + output RMSNorm' if norm else ''} + top-k 64/top-p 0.95, "
-                   f"B={B} hidden rows N(0,1)"}
+                   f"B={B} hidden rows N(0,1), weights {'packed (lmhead_pack)' if packed else 'in the GGUF layout'}"}
     return out
 
 
@@ -414,6 +419,8 @@ def main():
     ap.add_argument("--lmhead", type=int, metavar="B",
                     help="only the lm_head + sampling workload at B hidden rows (one JSON line)")
     ap.add_argument("--lmhead-format", default="q4_0", choices=sorted(LMHEAD_FORMATS))
+    ap.add_argument("--lmhead-gguf-layout", action="store_true",
+                    help="read the weights in their GGUF layout instead of the packed one")
     ap.add_argument("--lmhead-norm", action="store_true", help="fuse the output RMSNorm")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU: turn two rocprofv3 --pmc counter CSVs into profiles/traffic_<workload>.json")
@@ -428,7 +435,7 @@ def main():
 
     if a.lmhead:
         print(json.dumps(run_lmhead(a.lmhead, min(a.steps, 500), min(a.warmup, 20), fmt=a.lmhead_format,
-                                    norm=a.lmhead_norm)), flush=True)
+                                    norm=a.lmhead_norm, packed=not a.lmhead_gguf_layout)), flush=True)
         return
     r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
@@ -472,6 +479,7 @@ def main():
                             / HBM_PEAK_GBS}
         for B in (1, 16):
             others[f"lmhead_b{B}"] = run_lmhead(B, 200, 10)
+        others["lmhead_b1_gguf_layout"] = run_lmhead(1, 200, 10, packed=False)
         for fmt in ("q8_0", "f16"):
             others[f"lmhead_{fmt}_norm_b1"] = run_lmhead(1, 200, 10, fmt=fmt, norm=True)
         out["other_workloads"] = others

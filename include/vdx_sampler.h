@@ -141,6 +141,8 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
 #define VDX_TENSOR_F16 1   /* in_dim fp16 values per row (matvec_f16.comp)          */
 #define VDX_TENSOR_Q4_0 2  /* 18-byte blocks: fp16 d, 16 bytes of nibbles          */
 #define VDX_TENSOR_Q8_0 8  /* 34-byte blocks: fp16 d, 32 int8 (matvec_q8_0.comp)   */
+/* OR-ed into wtype: `weights` are in the packed layout of vdx_lmhead_pack. */
+#define VDX_LMHEAD_PACKED 0x100
 
 /* TVdxModel.UnembedToLogits (Model.pas:1258-1270) batched over `rows` hidden
  * vectors: the output RMSNorm as TVdxLayerNorm.ApplyCopy issues it
@@ -158,6 +160,23 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
 int vdx_lmhead(const void *weights, int32_t wtype, const float *hidden, const float *norm_weight,
                float norm_eps, int32_t rows, int32_t in_dim, int32_t vocab, float *logits,
                int64_t logit_stride, float *scratch, void *stream);
+
+/* The lm_head weights repacked for MI355X, once, when the model is loaded (no
+ * counterpart in the reference, whose UploadWeightTensor, Model.pas:549-600,
+ * uploads the GGUF bytes as they are): the same bytes permuted so that, for
+ * each group of 64 rows (the last padded with zero rows), each K slice and
+ * each 16-byte (Q8_0: 8-byte) piece, the 64 rows' pieces are consecutive.  A
+ * row of a Q4_0 or Q8_0 tensor is not a whole number of 128-byte cache
+ * lines, so reading K slices of rows from the GGUF layout fetches the lines
+ * at slice boundaries twice; in the packed layout every line is read once, by
+ * one coalesced load.  vdx_lmhead and vdx_sampler_lmhead_device read it when
+ * wtype carries VDX_LMHEAD_PACKED and give bit-identical logits.
+ * vdx_lmhead_packed_bytes returns the packed size (or VDX_E_INVALID_ARG);
+ * vdx_lmhead_pack writes it (device buffers, 16-byte aligned; stream-ordered,
+ * allocates nothing). */
+int64_t vdx_lmhead_packed_bytes(int32_t wtype, int32_t in_dim, int32_t vocab);
+int vdx_lmhead_pack(const void *weights, int32_t wtype, int32_t in_dim, int32_t vocab, void *packed,
+                    int64_t packed_bytes, void *stream);
 
 /* RunUnembedding followed by Process (Inference.pas:327-339) with the logits
  * kept in HBM: UnembedToLogits (as vdx_lmhead, the sampler's own workspace as

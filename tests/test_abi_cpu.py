@@ -120,3 +120,15 @@ def test_lmhead_argument_errors_need_no_gpu():
     rc = L.vdx_lmhead(C.c_void_p(al), 8, hid, hid, C.c_float(1e-6), 1, 256, 1024, C.c_void_p(al), 1024,
                       None, None)
     assert rc == -1 and "scratch" in L.vdx_sampler_last_error(None).decode()
+
+
+def test_lmhead_packed_bytes_needs_no_gpu():
+    # the packed size: 64-row groups (the last padded) of whole rows
+    from vindexllm_amd import VDX_LMHEAD_PACKED, lmhead_packed_bytes
+    from vindexllm_amd.sampler import VdxSamplerError
+    assert lmhead_packed_bytes(2, 2560, 262144) == 262144 * 80 * 18
+    assert lmhead_packed_bytes(8, 2560, 262144 + 1) == (262144 + 64) * 80 * 34
+    assert lmhead_packed_bytes(1, 256, 1) == 64 * 256 * 2
+    for bad in ((3, 2560, 10), (2, 100, 10), (2, 2560, 0), (2 | VDX_LMHEAD_PACKED << 1, 256, 1)):
+        with pytest.raises(VdxSamplerError):
+            lmhead_packed_bytes(*bad)

@@ -319,3 +319,108 @@ def test_lmhead_from_gguf_file(tmp_path, wtype):
         want = O.matvec(w, wtype, O.rmsnorm(H[b], nw, 1e-6), D, V, True)
         assert np.array_equal(G[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
     log(f"[done] lm_head from GGUF wtype={wtype}")
+
+
+def _pack_ref(w, wtype, D, V):
+    """The packed layout restated with numpy: for each 64-row group, slice s
+    and piece k, the 64 rows' pieces in row order (rows past V are zero)."""
+    bb = {O.TENSOR_Q4_0: 18, O.TENSOR_Q8_0: 34, O.TENSOR_F16: 64}[wtype]
+    P, PB, SE = {O.TENSOR_Q4_0: (9, 16, 256), O.TENSOR_Q8_0: (17, 8, 128), O.TENSOR_F16: (8, 16, 64)}[wtype]
+    rowbytes = D // 32 * bb
+    nw = (V + 63) // 64
+    rows = np.zeros((nw * 64, rowbytes), dtype=np.uint8)
+    rows[:V] = w.reshape(V, rowbytes)
+    ns = D // SE
+    t = rows.reshape(nw, 64, ns, P, PB)            # wave, lane, slice, piece, bytes
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(-1)
+
+
+@pytest.mark.parametrize("wtype", [O.TENSOR_Q4_0, O.TENSOR_Q8_0, O.TENSOR_F16])
+def test_lmhead_pack_layout(wtype):
+    # the pack kernel's output equals the layout restated with numpy
+    import torch
+
+    from vindexllm_amd import lmhead_pack, lmhead_packed_bytes
+
+    V, D = 200, 512
+    log(f"[case] lm_head pack layout wtype={wtype}")
+    rng = np.random.default_rng(9300 + wtype)
+    w = {O.TENSOR_Q8_0: rand_q8_0, O.TENSOR_F16: rand_f16, O.TENSOR_Q4_0: rand_q4_0}[wtype](rng, V, D)
+    p = lmhead_pack(torch.from_numpy(w).cuda(), wtype, D, V)
+    torch.cuda.synchronize()
+    want = _pack_ref(w, wtype, D, V)
+    assert lmhead_packed_bytes(wtype, D, V) == want.size == p.numel()
+    assert np.array_equal(p.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("wtype", [O.TENSOR_Q4_0, O.TENSOR_Q8_0, O.TENSOR_F16])
+@pytest.mark.parametrize("V,D,B,norm", [(4096 + 77, 256, 1, False), (4096 + 77, 768, 3, True),
+                                        (2048, 512, 8, False), (1000, 2560, 16, True),
+                                        (300, 2560, 1, True), (63, 256, 17, False)])
+def test_lmhead_packed_matches_gguf_layout(wtype, V, D, B, norm):
+    # the packed layout gives the same logits bit for bit (and so the oracle's)
+    import torch
+
+    from vindexllm_amd import VDX_LMHEAD_PACKED, lmhead, lmhead_pack
+
+    log(f"[case] packed lm_head wtype={wtype} V={V} D={D} B={B} norm={norm}")
+    rng = np.random.default_rng(9400 + wtype * 100 + V + D + B)
+    w = {O.TENSOR_Q8_0: rand_q8_0, O.TENSOR_F16: rand_f16, O.TENSOR_Q4_0: rand_q4_0}[wtype](rng, V, D)
+    H = (rng.standard_normal((B, D)) * 4.0).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    dev = torch.device("cuda:0")
+    wd, hd = torch.from_numpy(w).to(dev), torch.from_numpy(H).to(dev)
+    nd = torch.from_numpy(nw).to(dev) if norm else None
+    wp = lmhead_pack(wd, wtype, D, V)
+    a = lmhead(wd, wtype, hd, V, norm_weight=nd)
+    b = lmhead(wp, wtype | VDX_LMHEAD_PACKED, hd, V, norm_weight=nd)
+    torch.cuda.synchronize()
+    G = b.cpu().numpy()
+    assert np.array_equal(a.cpu().numpy().view(np.uint32), G.view(np.uint32))
+    for r in range(min(B, 3)):
+        xn = O.rmsnorm(H[r], nw, 1e-6) if norm else H[r]
+        want = O.matvec(w, wtype, xn, D, V, True)
+        assert np.array_equal(G[r].view(np.uint32), want.view(np.uint32)), f"row {r}"
+    log(f"[done] packed lm_head wtype={wtype} V={V} D={D} B={B}")
+
+
+def test_lmhead_packed_from_gguf_with_sampling(tmp_path):
+    # the head read from a model file, packed on the device, then the fused
+    # norm + lm_head + sampling call: the same tokens and logits as the GGUF
+    # layout
+    import torch
+
+    import ggufw
+
+    from vindexllm_amd import TVdxGGUFReader, TVdxSampler, lm_head_from_gguf
+
+    V, D, B = 8192 + 5, 2560, 4
+    log("[case] packed lm_head from GGUF + sampling")
+    rng = np.random.default_rng(9500)
+    w = rand_q4_0(rng, V, D)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    blob, _ = ggufw.build([], [("output_norm.weight", [D], 0, nw.tobytes()),
+                              ("token_embd.weight", [D, V], O.TENSOR_Q4_0, w.tobytes())])
+    p = tmp_path / "m.gguf"
+    p.write_bytes(blob)
+    r = TVdxGGUFReader()
+    assert r.Open(str(p))
+    dev = torch.device("cuda:0")
+    plain = lm_head_from_gguf(r, dev)
+    packed = lm_head_from_gguf(r, dev, pack=True)
+    H = torch.from_numpy((rng.standard_normal((B, D)) * 3.0).astype(np.float32)).to(dev)
+    u = torch.from_numpy(u_stream(rng, B)).to(dev)
+    res = []
+    for lm in (plain, packed):
+        with TVdxSampler(0, B) as s:
+            c = s.DefaultConfig()
+            c.Temperature, c.TopK, c.TopP = 1.0, 64, 0.95
+            s.SetConfig(c)
+            L = torch.empty(B, V, device=dev)
+            tok = s.lmhead_device(lm["weights"], lm["wtype"], H, V, norm_weight=lm["norm_weight"], logits=L,
+                                  uniforms=u)
+            torch.cuda.synchronize()
+            res.append((tok.cpu().numpy(), L.cpu().numpy()))
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1].view(np.uint32), res[1][1].view(np.uint32))
+    log("[done] packed lm_head from GGUF + sampling")

@@ -572,8 +572,11 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
   return tok;
 }
 
+// wtype = a VDX_TENSOR_* format, optionally | VDX_LMHEAD_PACKED
+static int lm_format(int32_t wtype) { return wtype & ~VDX_LMHEAD_PACKED; }
 static int lm_block_bytes(int32_t wtype) {
-  return wtype == kLmQ4_0 ? 18 : wtype == kLmQ8_0 ? 34 : wtype == kLmF16 ? 64 : 0;
+  const int f = lm_format(wtype);
+  return f == kLmQ4_0 ? 18 : f == kLmQ8_0 ? 34 : f == kLmF16 ? 64 : 0;
 }
 
 // nullptr when the arguments are valid; *rc is set to the error code otherwise
@@ -611,10 +614,35 @@ int vdx_lmhead(const void *weights, int32_t wtype, const float *hidden, const fl
     return VDX_E_INVALID_ARG;
   }
   LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, logit_stride, rows, in_dim,
-                  vocab, scratch, wtype, norm_weight, norm_eps};
+                  vocab, scratch, lm_format(wtype), norm_weight, norm_eps,
+                  (wtype & VDX_LMHEAD_PACKED) ? 1 : 0};
   const hipError_t e = launch_lmhead(lp, (hipStream_t)stream);
   if (e != hipSuccess) {
     g_call_err = std::string("lm_head launch: ") + hipGetErrorString(e);
+    return VDX_E_HIP;
+  }
+  g_call_err.clear();
+  return VDX_OK;
+}
+
+int64_t vdx_lmhead_packed_bytes(int32_t wtype, int32_t in_dim, int32_t vocab) {
+  if (lm_block_bytes(wtype) == 0 || in_dim <= 0 || in_dim % 256 != 0 || vocab <= 0) return VDX_E_INVALID_ARG;
+  return lmhead_packed_bytes(lm_format(wtype), in_dim, vocab);
+}
+
+int vdx_lmhead_pack(const void *weights, int32_t wtype, int32_t in_dim, int32_t vocab, void *packed,
+                    int64_t packed_bytes, void *stream) {
+  const int64_t need = vdx_lmhead_packed_bytes(wtype, in_dim, vocab);
+  if (need < 0 || !weights || !packed || packed_bytes < need || (uintptr_t)weights % 16 != 0 ||
+      (uintptr_t)packed % 16 != 0 || (wtype & VDX_LMHEAD_PACKED)) {
+    g_call_err = "lm_head pack: need a VDX_TENSOR_* format, in_dim % 256 == 0, 16-byte aligned buffers "
+                 "and packed_bytes >= vdx_lmhead_packed_bytes()";
+    return VDX_E_INVALID_ARG;
+  }
+  const hipError_t e = launch_lmhead_pack((const uint8_t *)weights, lm_format(wtype), in_dim, vocab,
+                                          (uint8_t *)packed, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    g_call_err = std::string("lm_head pack launch: ") + hipGetErrorString(e);
     return VDX_E_HIP;
   }
   g_call_err.clear();
@@ -666,7 +694,7 @@ int vdx_sampler_lmhead_device(vdx_sampler *s, const void *weights, int32_t wtype
     s->xt_dim = in_dim;
   }
   LmHeadParams lp{(const uint8_t *)weights, hidden, in_dim, logits, ls, rows, in_dim, vocab, s->d_xt,
-                  wtype, norm_weight, norm_eps};
+                  lm_format(wtype), norm_weight, norm_eps, (wtype & VDX_LMHEAD_PACKED) ? 1 : 0};
   HIP_TRY(s, launch_lmhead(lp, (hipStream_t)stream));
   return vdx_sampler_process_device(s, logits, rows, vocab, ls, uniforms, out, stream);
 }

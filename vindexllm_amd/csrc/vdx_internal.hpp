@@ -52,9 +52,15 @@ struct LmHeadParams {
   int32_t format;          // kLmQ4_0, kLmQ8_0 or kLmF16
   const float *norm_weight;  // output RMSNorm weight [in_dim] (nullable: no norm)
   float norm_eps;
+  int32_t packed;          // weights in the packed layout of launch_lmhead_pack
 };
 
 hipError_t launch_lmhead(const LmHeadParams &p, hipStream_t st);
+// The lm_head weights repacked for coalesced, line-aligned loads (see
+// k_lmhead_pack): lmhead_packed_bytes() bytes at `packed`.
+int64_t lmhead_packed_bytes(int format, int in_dim, int vocab);
+hipError_t launch_lmhead_pack(const uint8_t *w, int format, int in_dim, int vocab, uint8_t *packed,
+                              hipStream_t st);
 hipError_t launch_penalty(const CallParams &p, hipStream_t st);
 hipError_t launch_greedy(const CallParams &p, hipStream_t st);
 hipError_t launch_topk(const CallParams &p, hipStream_t st);

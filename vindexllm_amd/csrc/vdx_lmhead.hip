@@ -176,7 +176,7 @@ template <> struct PieceT<kLmQ8_0> { typedef u32x2 T; };
 template <> struct PieceT<kLmF16> { typedef u32x4 T; };
 
 // x: hidden row (NB == 1, no norm) or the prepared copy [in_dim][NB].
-template <int FMT, int NB>
+template <int FMT, int NB, bool PACKED>
 __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, const float *__restrict__ x,
                                                float *__restrict__ logits, int64_t ls, int32_t in_dim,
                                                int32_t vocab, int32_t B) {
@@ -184,13 +184,54 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
   typedef typename PieceT<FMT>::T Piece;
   constexpr int P = F::kPieces, PD = F::kPieceDw, PB = 4 * PD;  // pieces, dwords and bytes per piece
   constexpr int SE = 32 * F::kNBlk;                              // elements per slice
-  __shared__ Piece tile[64 * P];
   const int t = threadIdx.x;
   const int v0 = blockIdx.x * 64;
   const int nrows = min(64, vocab - v0);
   // unsigned arithmetic: in_dim > 0 (the signed forms cost registers here)
   const int rowbytes = (int)(((uint32_t)in_dim >> 5) * (uint32_t)F::kBlockBytes);
   const int nslices = (int)((uint32_t)in_dim / (uint32_t)SE);
+  float acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+
+  if constexpr (PACKED) {
+    // packed layout (k_lmhead_pack): piece k of slice s of the wave's row t
+    // at ((s * P + k) * 64 + t) * PB from the wave's base, so each load
+    // instruction reads 64 consecutive pieces and every cache line is fetched
+    // once; the lane receives its own row's slice, with no transpose
+    const uint8_t *wp = wq + (int64_t)blockIdx.x * (int64_t)nslices * (P * 64 * PB) + t * PB;
+    Piece ca[P], cb[P];
+    auto load = [&](Piece (&dst)[P], int sl) {
+#pragma unroll
+      for (int k = 0; k < P; ++k)
+        dst[k] = __builtin_nontemporal_load(reinterpret_cast<const Piece *>(wp + (sl * P + k) * (64 * PB)));
+    };
+    auto compute = [&](const Piece (&src)[P], int sl) {
+      uint32_t r[P * PD];
+#pragma unroll
+      for (int j = 0; j < P; ++j)
+#pragma unroll
+        for (int k = 0; k < PD; ++k) r[PD * j + k] = src[j][k];
+      lm_slice<FMT, NB>(r, x + SE * NB * sl, acc);
+    };
+    load(ca, 0);
+    for (int s = 0; s < nslices; s += 2) {
+      if (s + 1 < nslices) load(cb, s + 1);
+      compute(ca, s);
+      if (s + 1 < nslices) {
+        if (s + 2 < nslices) load(ca, s + 2);
+        compute(cb, s + 1);
+      }
+    }
+    if (t < nrows) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        if (b < B) logits[(int64_t)b * ls + v0 + t] = acc[b];
+    }
+    return;
+  }
+
+  __shared__ Piece tile[64 * P];
   const uint8_t *wt = wq + (int64_t)v0 * rowbytes;
 
   // piece Q = t + 64 i of a slice tile is piece j = Q % P of row Q / P; rows
@@ -211,9 +252,6 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
   };
   load_slice(0);
 
-  float acc[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
   for (int s = 0; s < nslices; ++s) {
     __syncthreads();  // the previous slice has been read (one wave: no-op ordering)
 #pragma unroll
@@ -273,10 +311,58 @@ __global__ __launch_bounds__(256) void k_lmhead_prep(const float *__restrict__ h
   for (int e = t; e < in_dim; e += 256) xt[(int64_t)e * NB + b] = (h[e] * inv_rms) * w[e];
 }
 
+// The packed layout of a weight tensor (vocab rows of in_dim elements in
+// format FMT): for each group of 64 rows (the last padded with zero rows),
+// each slice s and each piece k, the 64 rows' pieces in row order.  One
+// thread per destination piece; rows past the vocabulary are zero.
 template <int FMT>
+__global__ __launch_bounds__(256) void k_lmhead_pack(const uint8_t *__restrict__ wq, uint8_t *__restrict__ out,
+                                                      int32_t in_dim, int32_t vocab, int64_t npieces) {
+  typedef LmFmt<FMT> F;
+  typedef typename PieceT<FMT>::T Piece;
+  constexpr int P = F::kPieces, PB = 4 * F::kPieceDw, SE = 32 * F::kNBlk;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= npieces) return;
+  const int64_t nslices = in_dim / SE;
+  const int t = (int)(i & 63);
+  const int64_t q = i >> 6;  // (wave * nslices + s) * P + k
+  const int k = (int)(q % P);
+  const int64_t ws = q / P;
+  const int64_t s = ws % nslices, w = ws / nslices;
+  const int64_t row = w * 64 + t;
+  const int64_t rowbytes = (int64_t)(in_dim / 32) * F::kBlockBytes;
+  Piece v;
+  if (row < vocab)
+    v = *reinterpret_cast<const Piece *>(wq + row * rowbytes + (s * P + k) * PB);
+  else
+    v = Piece{};
+  *reinterpret_cast<Piece *>(out + i * PB) = v;
+}
+
+int64_t lmhead_packed_bytes(int format, int in_dim, int vocab) {
+  const int bb = format == kLmQ4_0 ? 18 : format == kLmQ8_0 ? 34 : 64;
+  return (int64_t)((vocab + 63) / 64) * 64 * (int64_t)(in_dim / 32) * bb;
+}
+
+hipError_t launch_lmhead_pack(const uint8_t *w, int format, int in_dim, int vocab, uint8_t *packed,
+                              hipStream_t st) {
+  const int pb = format == kLmQ8_0 ? 8 : 16;
+  const int64_t npieces = lmhead_packed_bytes(format, in_dim, vocab) / pb;
+  const dim3 grid((unsigned)((npieces + 255) / 256));
+  if (format == kLmQ4_0)
+    hipLaunchKernelGGL(k_lmhead_pack<kLmQ4_0>, grid, dim3(256), 0, st, w, packed, in_dim, vocab, npieces);
+  else if (format == kLmQ8_0)
+    hipLaunchKernelGGL(k_lmhead_pack<kLmQ8_0>, grid, dim3(256), 0, st, w, packed, in_dim, vocab, npieces);
+  else
+    hipLaunchKernelGGL(k_lmhead_pack<kLmF16>, grid, dim3(256), 0, st, w, packed, in_dim, vocab, npieces);
+  return hipGetLastError();
+}
+
+template <int FMT, bool PACKED>
 static void launch_fmt(int NB, dim3 grid, hipStream_t st, const uint8_t *w, const float *x, float *l,
                        int64_t ls, int32_t in_dim, int32_t vocab, int32_t B) {
-#define VDX_LM(N) hipLaunchKernelGGL((k_lmhead<FMT, N>), grid, dim3(64), 0, st, w, x, l, ls, in_dim, vocab, B)
+#define VDX_LM(N) \
+  hipLaunchKernelGGL((k_lmhead<FMT, N, PACKED>), grid, dim3(64), 0, st, w, x, l, ls, in_dim, vocab, B)
   if (NB == 1)
     VDX_LM(1);
   else if (NB == 2)
@@ -302,12 +388,16 @@ hipError_t launch_lmhead(const LmHeadParams &p, hipStream_t st) {
                          p.norm_weight, p.norm_eps, p.in_dim, B, NB, p.scratch);
       x = p.scratch;
     }
+#define VDX_FMT(FM)                                                                          \
+  (p.packed ? launch_fmt<FM, true>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B) \
+            : launch_fmt<FM, false>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B))
     if (p.format == kLmQ4_0)
-      launch_fmt<kLmQ4_0>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
+      VDX_FMT(kLmQ4_0);
     else if (p.format == kLmQ8_0)
-      launch_fmt<kLmQ8_0>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
+      VDX_FMT(kLmQ8_0);
     else
-      launch_fmt<kLmF16>(NB, grid, st, p.weights, x, l, p.logit_stride, p.in_dim, p.vocab, B);
+      VDX_FMT(kLmF16);
+#undef VDX_FMT
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -346,7 +346,7 @@ class TVdxGGUFReader:
         return src.to(device)
 
 
-def lm_head_from_gguf(reader: TVdxGGUFReader, device, norm: bool = True):
+def lm_head_from_gguf(reader: TVdxGGUFReader, device, norm: bool = True, pack: bool = False):
     """What the lm_head needs from a model file, on `device`:
 
     weights    token_embd.weight in its GGUF layout (uint8), the tied output
@@ -358,6 +358,9 @@ def lm_head_from_gguf(reader: TVdxGGUFReader, device, norm: bool = True):
                in_dim singles like UploadNormWeight, Model.pas:514-540), or
                None when `norm` is False
     norm_eps   1e-6, the reference's RMSNorm epsilon (LayerNorm.pas:186)
+
+    With ``pack`` the weights are repacked on the device (``lmhead_pack``)
+    and ``wtype`` carries VDX_LMHEAD_PACKED.
     """
     import numpy as np
     import torch
@@ -372,6 +375,10 @@ def lm_head_from_gguf(reader: TVdxGGUFReader, device, norm: bool = True):
     in_dim, vocab = info.Dimensions
     out = dict(weights=reader.tensor_to_device("token_embd.weight", device), wtype=info.TensorType,
                in_dim=int(in_dim), vocab=int(vocab), norm_weight=None, norm_eps=1e-6)
+    if pack:
+        from .sampler import VDX_LMHEAD_PACKED, lmhead_pack
+        out["weights"] = lmhead_pack(out["weights"], info.TensorType, int(in_dim), int(vocab))
+        out["wtype"] = info.TensorType | VDX_LMHEAD_PACKED
     if norm:
         ninfo = reader.GetTensorInfo("output_norm.weight")
         if ninfo is None:

@@ -30,6 +30,7 @@ VDX_RNG_PHILOX = 1
 VDX_TENSOR_F16 = 1   # lm_head weight formats: GGML type ids (GGUFReader.pas:34-42)
 VDX_TENSOR_Q4_0 = 2
 VDX_TENSOR_Q8_0 = 8
+VDX_LMHEAD_PACKED = 0x100  # OR-ed into wtype: weights in the layout of lmhead_pack
 
 ROW_GREEDY = 0x1
 ROW_TOPK_FAST = 0x2
@@ -118,6 +119,9 @@ _SIGNATURES = {
                                   C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
     "vdx_lmhead": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_float, C.c_int32,
                              C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "vdx_lmhead_packed_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
+    "vdx_lmhead_pack": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int64,
+                                  C.c_void_p]),
     "vdx_sampler_lmhead_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                                             C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                             C.c_int64, C.c_void_p, C.POINTER(_Outputs), C.c_void_p]),
@@ -453,6 +457,32 @@ def lmhead(weights, wtype: int, hidden, vocab: int, norm_weight=None, norm_eps: 
     if rc != VDX_OK:
         raise VdxSamplerError(rc, _err(None))
     return logits
+
+
+def lmhead_packed_bytes(wtype: int, in_dim: int, vocab: int) -> int:
+    n = load_library().vdx_lmhead_packed_bytes(int(wtype), int(in_dim), int(vocab))
+    if n < 0:
+        raise VdxSamplerError(int(n), "lm_head pack: need a VDX_TENSOR_* format and in_dim % 256 == 0")
+    return int(n)
+
+
+def lmhead_pack(weights, wtype: int, in_dim: int, vocab: int, out=None, stream=None):
+    """The lm_head weights (uint8 GPU tensor in the GGUF layout of ``wtype``)
+    repacked once for coalesced, line-aligned loads; pass the result with
+    ``wtype | VDX_LMHEAD_PACKED`` to ``lmhead`` / ``TVdxSampler.lmhead_device``
+    (bit-identical logits)."""
+    import torch
+
+    assert weights.is_cuda and weights.dtype == torch.uint8
+    n = lmhead_packed_bytes(wtype, in_dim, vocab)
+    if out is None:
+        out = torch.empty(n, dtype=torch.uint8, device=weights.device)
+    st = stream if stream is not None else torch.cuda.current_stream(weights.device)
+    rc = load_library().vdx_lmhead_pack(C.c_void_p(weights.data_ptr()), int(wtype), int(in_dim), int(vocab),
+                                        C.c_void_p(out.data_ptr()), int(out.numel()), C.c_void_p(st.cuda_stream))
+    if rc != VDX_OK:
+        raise VdxSamplerError(rc, _err(None))
+    return out
 
 
 def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=None):
