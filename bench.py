@@ -240,7 +240,7 @@ VALU_FP32_PEAK_TFLOPS = 157.3      # MI355X published FP32 vector peak (packed F
 LMHEAD_FORMATS = {"q4_0": (2, 18), "q8_0": (8, 34), "f16": (1, 64)}  # GGML type id, bytes per 32
 
 
-def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True):
+def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True, eager=False):
     """lm_head + sampling with the logits kept in HBM (RunUnembedding followed
     by Process, Inference.pas:327-339): the lm_head of 262144 x 2560 in `fmt`
     (Q4_0: nibbles uniform 0..15; Q8_0: int8 uniform; fp16 scales
@@ -248,7 +248,8 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True):
     B hidden rows N(0, 1), then top-k 64 / top-p 0.95 / T 1.0.  With `packed`
     the weights are first repacked once (lmhead_pack, outside the timed
     region) and read in that layout.  Times the whole call and the lm_head
-    alone (norm included), each from a captured hipGraph."""
+    alone (norm included), each from a captured hipGraph (or issued one by
+    one with `eager`, for counter collection)."""
     import torch
 
     from vindexllm_amd import VDX_LMHEAD_PACKED, TVdxSampler, lmhead, lmhead_pack
@@ -294,19 +295,24 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True):
             for _ in range(max(warmup, 1)):
                 fn()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=cs):
-            fn()
-        graph.replay()
-        torch.cuda.synchronize()
-        # replay() launches on torch's current stream: the events go there
-        rs = torch.cuda.current_stream(dev)
+        if eager:
+            rs = cs
+            run = fn
+        else:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=cs):
+                fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            # replay() launches on torch's current stream: the events go there
+            rs = torch.cuda.current_stream(dev)
+            run = graph.replay
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record(rs)
         for _ in range(steps):
-            graph.replay()
+            run()
         e1.record(rs)
         torch.cuda.synchronize()
         res[tag] = dict(wall_us=1e6 * (time.perf_counter() - t0) / steps,
@@ -435,7 +441,10 @@ def main():
 
     if a.lmhead:
         print(json.dumps(run_lmhead(a.lmhead, min(a.steps, 500), min(a.warmup, 20), fmt=a.lmhead_format,
-                                    norm=a.lmhead_norm, packed=not a.lmhead_gguf_layout)), flush=True)
+                                    norm=a.lmhead_norm, packed=not a.lmhead_gguf_layout, eager=a.eager)),
+              flush=True)
+        if a.copy_calibration:
+            copy_calibration()
         return
     r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
