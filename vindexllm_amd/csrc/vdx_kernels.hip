@@ -1742,6 +1742,17 @@ __global__ __launch_bounds__(kBlock) void k_topk_scalar(CallParams p) { topk_bod
 // and rescans that one segment.  With Min-P on, k_full_max first finds M and
 // the weights are the reference's q with q < MinP zeroed (Qmax = 1).
 // =============================================================================
+// e^x for the single pass's weights, x = s - m <= 0 (or -inf): the hardware
+// 2^y (v_exp_f32, 1 ulp) of y = fl32(x log2 e).  The product's rounding
+// shifts y by at most 2^-25 |y|, so a weight is within (|y| 2^-25 ln 2 +
+// 2^-23) of e^x relative, and e^x |x| <= 1/e bounds what any weight adds to
+// a running sum's error: far inside the draw's 1e-6 boundary tolerance.
+// Weights below 2^-126 may come out as 0.  (The exact pass, with Min-P,
+// computes the reference's fl32(exp(double)) instead.)
+__device__ __forceinline__ float exp_nonpos(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 struct FullSmem {
   union {
     PenaltySmem pen;          // stream phase: the fused penalty's table
@@ -1836,19 +1847,22 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   load_chunk<VEC, true>(L + c0, clen, wv, lane, v, -INFINITY);
   if (pen) penalty_pass<true>(p, row, c0, clen, pf, v, sm.pen);
 
-  // s = fl32(L * invT); positions past the row end weigh nothing
-  float m = -INFINITY;
-  bool bad = false;
+  // s = fl32(L * invT); positions past the row end (loaded as -inf) weigh
+  // nothing.  v_maximum propagates NaN, so one test of the thread maximum
+  // finds a NaN anywhere in its logits.  Only with invT = 0 (T = +inf) would
+  // a padding position turn into NaN (-inf * 0): the short last chunk then
+  // resets those positions.
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
-    if (chunk_pos<true>(wv, lane, i) < clen) {
-      v[i] = v[i] * p.inv_t;
-      m = fmaxf(m, v[i]);
-      bad = bad || (v[i] != v[i]);
-    } else {
-      v[i] = -INFINITY;
-    }
+  for (int i = 0; i < kPerThread; ++i) v[i] = v[i] * p.inv_t;
+  if (clen < kChunk && !(p.inv_t > 0.0f)) {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+      if (chunk_pos<true>(wv, lane, i) >= clen) v[i] = -INFINITY;
   }
+  float m = v[0];
+#pragma unroll
+  for (int i = 1; i < kPerThread; ++i) m = vmax(m, v[i]);
+  const bool bad = (m != m);
   float base;
   if (EXACT) {
     // row maximum from the k_full_max records of this row
@@ -1877,7 +1891,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
         const float q = (float)exp((double)v[i] - (double)base);
         w = (q < p.min_p) ? 0.0f : q;
       } else {
-        w = expf(v[i] - base);
+        w = exp_nonpos(v[i] - base);
       }
       acc += (double)w;
     }
@@ -2013,7 +2027,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
           const float q = (float)exp((double)s - (double)M);
           w = (q < p.min_p) ? 0.0f : q;
         } else {
-          w = expf(s - tcm);
+          w = exp_nonpos(s - tcm);
         }
       }
       w4[i] = w;
