@@ -336,6 +336,33 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True, eager=Fals
     return out
 
 
+def run_host_process(steps=300, warmup=20):
+    """The host entry point as the reference calls it (Process on one host row,
+    Inference.pas:327-339): each call uploads the 1 MiB row over PCIe, samples
+    it (B=1 top-k 64 / top-p 0.95 / T 1.0) and returns the token to the host.
+    The PCIe-inclusive rate, reported beside `value`, never as it."""
+    import torch
+
+    from vindexllm_amd import TVdxSampler
+
+    w = WORKLOADS["single_row"]
+    L, _ = make_inputs("single_row")
+    row = np.ascontiguousarray(L[0])
+    s = TVdxSampler(0, 1)
+    configure(s, w)
+    for _ in range(warmup):
+        s.Process(row)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        s.Process(row)
+    dt = (time.perf_counter() - t0) / steps
+    s.Free()
+    return {"rows_per_s": 1.0 / dt, "us_per_call": 1e6 * dt,
+            "desc": "vdx_sampler_process on a pageable host row: B=1 V=262144, 1 MiB upload + sampling + token "
+                    "download per call, top-k 64 / top-p 0.95 / T 1.0"}
+
+
 def copy_calibration(nbytes=1 << 30, reps=5):
     """Device-to-device copies of a known size, for scaling rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
@@ -489,6 +516,7 @@ def main():
         for B in (1, 16):
             others[f"lmhead_b{B}"] = run_lmhead(B, 200, 10)
         others["lmhead_b1_gguf_layout"] = run_lmhead(1, 200, 10, packed=False)
+        others["host_process_b1"] = run_host_process()
         for fmt in ("q8_0", "f16"):
             others[f"lmhead_{fmt}_norm_b1"] = run_lmhead(1, 200, 10, fmt=fmt, norm=True)
         out["other_workloads"] = others
