@@ -278,3 +278,72 @@ def test_mixed_rows_graph_replay_matches_eager():
             assert torch.equal(buf, eager_logits), rep
             _ = (pristine * 2).sum().item()
     log("[done] mixed rows graph replay")
+
+
+def test_row_configs_through_the_lmhead_call():
+    # the fused norm + packed Q8_0 lm_head + sampling call with per-row
+    # configs: each row's token, top-K and logits as the oracle gives them for
+    # that row's config on the kernel-order logits
+    import torch
+
+    from test_gpu_lmhead import rand_q8_0
+    from vindexllm_amd import VDX_LMHEAD_PACKED, VDX_TENSOR_Q8_0, TVdxSampler, lmhead_pack
+
+    V, D = 16384 + 40, 2560
+    rows = [ROWS[1], ROWS[0], ROWS[3], ROWS[6], ROWS[2], ROWS[7]]
+    B = len(rows)
+    log(f"[case] per-row configs through lm_head, B={B}")
+    rng = np.random.default_rng(75)
+    w = rand_q8_0(rng, V, D)
+    H = (rng.standard_normal((B, D)) * 3.0).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    u = u_stream(rng, B)
+    hist = [rng.integers(0, V, kw.get("repeat_window", 64)).astype(np.int32) for kw in rows]
+    dev = torch.device("cuda:0")
+    wp = lmhead_pack(torch.from_numpy(w).to(dev), VDX_TENSOR_Q8_0, D, V)
+    L = torch.empty(B, V, device=dev)
+    ti = torch.full((B, 64), -1, dtype=torch.int32, device=dev)
+    tp = torch.full((B, 64), -1.0, dtype=torch.float32, device=dev)
+    fl = torch.zeros(B, dtype=torch.int32, device=dev)
+    with TVdxSampler(0, B) as s:
+        for r, kw in enumerate(rows):
+            _set(s, r, kw)
+            s.set_history(r, hist[r])
+        tok = s.lmhead_device(wp, VDX_TENSOR_Q8_0 | VDX_LMHEAD_PACKED, torch.from_numpy(H).to(dev), V,
+                              norm_weight=torch.from_numpy(nw).to(dev), logits=L, uniforms=torch.from_numpy(u).to(dev),
+                              topk_idx=ti, topk_prob=tp, flags=fl)
+        torch.cuda.synchronize()
+    g = dict(tokens=tok.cpu().numpy(), topk_idx=ti.cpu().numpy(), topk_prob=tp.cpu().numpy(),
+             flags=fl.cpu().numpy(), logits_after=L.cpu().numpy())
+    orc = []
+    for r, kw in enumerate(rows):
+        row = O.matvec(w, O.TENSOR_Q8_0, O.rmsnorm(H[r], nw, 1e-6), D, V, True)
+        t, tr = O.process_row(row, O.make_config(**_okw(kw)), float(u[r]), hist=hist[r], trace=True)
+        orc.append((t, tr, row))
+    nb = compare(g, orc, {}, label="rows through lm_head")
+    log(f"[done] per-row configs through lm_head: near-boundary {nb}/{B}")
+
+
+def test_host_process_on_a_row_config():
+    # Process (host row 0) with row 0 given its own config: the reference
+    # object's stream with that config, logits penalised in place
+    from vindexllm_amd import TVdxSampler
+
+    log("[case] host Process with a row config")
+    rng = np.random.default_rng(76)
+    kw = dict(temperature=0.9, top_k=20, top_p=0.9, repeat_penalty=1.3, repeat_window=8, seed=77)
+    ref = O.Sampler()
+    ref.set_config(O.make_config(**kw))
+    with TVdxSampler(0, 2) as s:
+        _set(s, None, dict(temperature=1.0, seed=5))
+        _set(s, 0, kw)
+        for i in range(20):
+            L = (rng.standard_normal(5000) * 2).astype(np.float32)
+            a, b = L.copy(), L.copy()
+            t_gpu = s.Process(a)
+            t_ref = ref.process(b)
+            assert t_gpu == t_ref, i
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+            s.AddToHistory(t_gpu)
+            ref.add_to_history(t_ref)
+    log("[done] host Process with a row config")
