@@ -77,5 +77,24 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+CPP_TESTBED_SRC = os.path.join(ROOT, "tests", "cpp", "test_sampler_testbed.cpp")
+CPP_TESTBED = os.path.join(ROOT, "tests", "cpp", "_build", "test_sampler_testbed")
+
+
+def build_cpp_testbed(out: str = CPP_TESTBED, rpath: str | None = None) -> str:
+    """The C++ host mirror's testbed (include/vdx_sampler.hpp, a port of the
+    reference's sampler testbed), linked against the built library; the
+    default rpath is relative to the binary, so the tree can move."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    if rpath is None:
+        rpath = "$ORIGIN/" + os.path.relpath(LIBDIR, os.path.dirname(out))
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"), "-o", out, CPP_TESTBED_SRC,
+           "-L", LIBDIR, "-lvdxsampler", "-Wl,-rpath," + rpath]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("g++ failed:\n" + " ".join(cmd) + "\n" + r.stdout + r.stderr)
+    return out
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
