@@ -26,7 +26,10 @@ HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by
 the same counter's reading for a 1 GiB device copy (bench.py --traffic-from
 turns the two counter CSVs into profiles/traffic_<workload>.json).
 cpu_baseline: the oracle (oracle/vdx_oracle.c, a C restatement of
-TVdxSampler.Process, gcc -O2) on one host core over a bounded sample.
+TVdxSampler.Process, gcc -O2) on one host core over a bounded sample;
+cpu_baseline_all_cores: the same split over the job's host threads.
+reference_readback: the step's device-to-host logits copy that the
+reference pipeline pays before its host sampler (pageable and pinned).
 """
 from __future__ import annotations
 
@@ -125,9 +128,18 @@ def configure(s, w):
         s.SetRowConfig(r, c)
 
 
-def cpu_baseline(name, L, hist, seconds):
-    """The oracle on one host core: rows processed serially, as the
-    reference's Process does; a bounded sample of ~`seconds` of CPU work."""
+def host_threads() -> int:
+    """Host threads for the all-cores baseline: the job's CPU share where the
+    environment states it (OMP_NUM_THREADS), else every core."""
+    n = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, int(n) if n.isdigit() else (os.cpu_count() or 1))
+
+
+def cpu_baseline(name, L, hist, seconds, threads=1):
+    """The oracle on the host: with threads=1 rows are processed serially, as
+    the reference's Process does; with more, the rows are split over that many
+    POSIX threads (one independent sampler each).  A bounded sample of
+    ~`seconds` of wall-clock work."""
     from oracle import vdx_oracle as O
 
     w = WORKLOADS[name]
@@ -142,13 +154,37 @@ def cpu_baseline(name, L, hist, seconds):
     while busy < seconds:
         X = L.copy()
         t0 = time.perf_counter()
-        O.process_batch(X, cfg, u, hist=hist, threads=1)
+        O.process_batch(X, cfg, u, hist=hist, threads=threads)
         busy += time.perf_counter() - t0
         rows_done += B
         passes += 1
-    return dict(value=rows_done / busy, unit="rows/s", cores=1, kind="port",
+    return dict(value=rows_done / busy, unit="rows/s", cores=threads, kind="port",
                 sample=f"{passes} passes x {B} rows of the same workload ({busy:.1f} s), "
-                       f"oracle/vdx_oracle.c gcc -O2, 1 thread")
+                       f"oracle/vdx_oracle.c gcc -O2, {threads} thread{'s' if threads > 1 else ''}")
+
+
+def readback_cost(rows, vocab, reps=50):
+    """What the reference pipeline pays before its host sampler runs: one
+    device-to-host copy of the step's logits (rows x vocab fp32,
+    Inference.pas:332-334) into pageable and into pinned host memory."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(rows, vocab, dtype=torch.float32, device=dev).normal_()
+    out = {"bytes": rows * vocab * 4}
+    for kind in ("pageable", "pinned"):
+        dst = torch.empty(rows, vocab, dtype=torch.float32, pin_memory=(kind == "pinned"))
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        us = 1e6 * (time.perf_counter() - t0) / reps
+        out[f"{kind}_us"] = us
+        out[f"{kind}_GBs"] = out["bytes"] / (us * 1e-6) / 1e9
+    return out
 
 
 def run_gpu(name, steps, warmup, eager):
@@ -525,6 +561,10 @@ def main():
     if not a.no_cpu:
         L, hist = make_inputs(a.workload)
         out["cpu_baseline"] = cpu_baseline(a.workload, L, hist, a.cpu_seconds)
+        nt = host_threads()
+        if nt > 1:
+            out["cpu_baseline_all_cores"] = cpu_baseline(a.workload, L, hist, a.cpu_seconds / 2, threads=nt)
+        out["reference_readback"] = readback_cost(r["rows"], r["vocab"])
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
