@@ -128,6 +128,18 @@ def configure(s, w):
         s.SetRowConfig(r, c)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), or '' where unreadable."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def host_threads() -> int:
     """Host threads for the all-cores baseline: the job's CPU share where the
     environment states it (OMP_NUM_THREADS), else every core."""
@@ -158,7 +170,7 @@ def cpu_baseline(name, L, hist, seconds, threads=1):
         busy += time.perf_counter() - t0
         rows_done += B
         passes += 1
-    return dict(value=rows_done / busy, unit="rows/s", cores=threads, kind="port",
+    return dict(value=rows_done / busy, unit="rows/s", cores=threads, kind="port", cpu=cpu_model(),
                 sample=f"{passes} passes x {B} rows of the same workload ({busy:.1f} s), "
                        f"oracle/vdx_oracle.c gcc -O2, {threads} thread{'s' if threads > 1 else ''}")
 
