@@ -432,7 +432,7 @@ def _kernel_base(name):
     name = name.strip()
     if name.startswith("void "):
         name = name[5:]
-    name = name.split("(")[0].strip()
+    name = name.split("(")[0].strip().replace(", ", ",")  # template arguments as in DOMINANT_KERNEL
     return name[5:] if name.startswith("vdx::") else name
 
 
