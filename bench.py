@@ -510,7 +510,7 @@ def main():
         traffic_from(a.workload, *a.traffic_from)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; the sampling path has no multi-GPU "
+        print("bench.py: measures one GPU; the sampling path has no multi-GPU "
               "collective (rows shard with zero exchange), so --gpus must be 1", file=sys.stderr)
         sys.exit(3)
 

@@ -2,8 +2,8 @@
  * vdx_oracle.h -- CPU oracle for the token-sampling path of VindexLLM.
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
- * sampler TVdxSampler (src/VindexLLM.Sampler.pas) used as the checker for the
- * HIP library and as the CPU baseline timed by bench.py.  Only tests/,
+ * sampler TVdxSampler (src/VindexLLM.Sampler.pas) that the HIP library's
+ * results are compared with, and the CPU baseline timed by bench.py.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
  * product library (libvdxsampler.so) never links or calls it.
  *

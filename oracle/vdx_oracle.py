@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY: the oracle is a plain-C restatement of the
 reference sampler ``TVdxSampler`` (src/VindexLLM.Sampler.pas).  Only tests/,
 ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this
-module, always as the checker or the timed CPU baseline, never as the
-product path.
+module, always as the reference the GPU results are compared with or as the
+timed CPU baseline, never as the product path.
 """
 from __future__ import annotations
 

@@ -1,5 +1,5 @@
 """Shared helpers of the GPU parity tests: run the HIP sampler and the CPU
-oracle on the same seeded inputs and compare them to the north-star bar:
+oracle on the same seeded inputs and compare them to the parity bar:
 tokens identical except draws within 1e-6*S of a CDF boundary (counted),
 top-K index sets and penalised logits bit-exact, probabilities within 1e-5
 relative."""

@@ -70,7 +70,7 @@ def test_cfg3_penalised_batch():
     assert (g["flags"] & (ROW_TOPK_FAST | ROW_TOPK_REPLAY)).all()
 
 
-def test_north_star_b256_topk():
+def test_b256_topk64_topp095():
     rng = np.random.default_rng(1006)
     L = cfg1_logits(rng, 256)
     u = u_stream(np.random.default_rng(2006), 256)

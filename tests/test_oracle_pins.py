@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/vdx_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/vdx_oracle.c) before the parity tests trust it.
 
 The reference has no golden vectors for its sampler (its only tests are the
 invariants in testbed/UTest.Sampler.pas).  Each oracle function is therefore

@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256) void k_lmhead_prep(const float *__restrict__ h
   float ss = 0.0f;
   for (int e = t; e < in_dim; e += 256) {
     const float v = h[e];
-    ss = ss + v * v;  // product, then sum (no contraction in this build)
+    ss = ss + v * v;  // product, then sum (-ffp-contract=off: no fused multiply-add)
   }
   part[t] = ss;
   __syncthreads();
