@@ -384,10 +384,13 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True, eager=Fals
     return out
 
 
-def run_host_process(steps=300, warmup=20):
+def run_host_process(steps=300, warmup=20, penalised=False):
     """The host entry point as the reference calls it (Process on one host row,
     Inference.pas:327-339): each call uploads the 1 MiB row over PCIe, samples
     it (B=1 top-k 64 / top-p 0.95 / T 1.0) and returns the token to the host.
+    penalised: RP 1.1 over a 64-id history as well, so each call also writes
+    the penalised history positions back into the caller's row (the row is
+    penalised again on every call, as the reference would).
     The PCIe-inclusive rate, reported beside `value`, never as it."""
     import torch
 
@@ -398,6 +401,12 @@ def run_host_process(steps=300, warmup=20):
     row = np.ascontiguousarray(L[0])
     s = TVdxSampler(0, 1)
     configure(s, w)
+    if penalised:
+        c = s.GetConfig()
+        c.RepeatPenalty, c.RepeatWindow = 1.1, 64
+        s.SetConfig(c)
+        for t in np.random.default_rng(11).integers(0, row.size, 64):
+            s.AddToHistory(int(t))
     for _ in range(warmup):
         s.Process(row)
     torch.cuda.synchronize()
@@ -408,7 +417,8 @@ def run_host_process(steps=300, warmup=20):
     s.Free()
     return {"rows_per_s": 1.0 / dt, "us_per_call": 1e6 * dt,
             "desc": "vdx_sampler_process on a pageable host row: B=1 V=262144, 1 MiB upload + sampling + token "
-                    "download per call, top-k 64 / top-p 0.95 / T 1.0"}
+                    "download per call, top-k 64 / top-p 0.95 / T 1.0"
+                    + (", RP 1.1 over 64 history ids (penalised positions written back)" if penalised else "")}
 
 
 def copy_calibration(nbytes=1 << 30, reps=5):
@@ -565,6 +575,7 @@ def main():
             others[f"lmhead_b{B}"] = run_lmhead(B, 200, 10)
         others["lmhead_b1_gguf_layout"] = run_lmhead(1, 200, 10, packed=False)
         others["host_process_b1"] = run_host_process()
+        others["host_process_b1_penalised"] = run_host_process(penalised=True)
         for fmt in ("q8_0", "f16"):
             others[f"lmhead_{fmt}_norm_b1"] = run_lmhead(1, 200, 10, fmt=fmt, norm=True)
         out["other_workloads"] = others

@@ -314,6 +314,34 @@ def test_host_process_matches_reference_stream():
                 ref.add_to_history(t_ref)
 
 
+def test_host_process_penalty_write_back():
+    # the caller's row after Process equals the reference's in-place penalty,
+    # bit for bit, with out-of-range, negative and repeated history ids and a
+    # window beyond the fused limit (the separate penalty kernel)
+    from vindexllm_amd import TVdxSampler
+
+    rng = np.random.default_rng(31)
+    V = 5000
+    for window, pen in ((8, 2.0), (300, 1.25)):
+        log(f"[case] host write-back window={window} RP={pen}")
+        ref = O.Sampler()
+        ref.set_config(O.make_config(temperature=0.9, top_k=20, seed=5, repeat_penalty=pen,
+                                     repeat_window=window))
+        with TVdxSampler(0, 1) as s:
+            _cfg(s, Temperature=0.9, TopK=20, Seed=5, RepeatPenalty=pen, RepeatWindow=window)
+            ids = [-5, V + 3, 7, 7, 0, V - 1] + rng.integers(0, V, window).tolist()
+            for t in ids[:window + 2]:
+                s.AddToHistory(int(t))
+                ref.add_to_history(int(t))
+            for i in range(5):
+                L = (rng.standard_normal(V) * 3).astype(np.float32)
+                L[7], L[0], L[V - 1] = 4.0, -2.5, 0.0
+                a, b = L.copy(), L.copy()
+                t_gpu, t_ref = s.Process(a), ref.process(b)
+                assert t_gpu == t_ref, (window, i)
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (window, i)
+
+
 def test_ref_invariants_on_gpu():
     # the five sections of testbed/UTest.Sampler.pas, against the GPU sampler
     from vindexllm_amd import TVdxSampler

@@ -55,6 +55,9 @@ struct vdx_sampler {
   float *d_row = nullptr;
   int32_t row_cap = 0;
   int32_t *d_tok = nullptr;
+  uint64_t *d_pairs = nullptr;  // penalised history positions of row 0 (id, value)
+  uint64_t *h_pairs = nullptr;  // pinned host copy
+  int32_t pairs_cap = 0;
   // instrumentation: three events per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev;
@@ -247,6 +250,8 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_lm);
   (void)hipFree(s->d_xt);
   (void)hipFree(s->d_tok);
+  (void)hipFree(s->d_pairs);
+  if (s->h_pairs) (void)hipHostFree(s->h_pairs);
   for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
   if (s->ev_fork) (void)hipEventDestroy(s->ev_fork);
   for (int i = 0; i < 2; ++i) {
@@ -564,11 +569,35 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab) {
   if (rc != VDX_OK) return rc;
   int32_t tok = -1;
   HIP_TRY(s, hipMemcpyAsync(&tok, s->d_tok, sizeof(int32_t), hipMemcpyDeviceToHost, s->stream));
-  // The reference penalises the caller's buffer in place (Sampler.pas:285-303).
-  if (s->row_cfg[0].repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0)
-    HIP_TRY(s, hipMemcpyAsync(logits, s->d_row, sizeof(float) * (size_t)vocab,
+  // The reference penalises the caller's buffer in place (Sampler.pas:285-303):
+  // only history positions change, so their penalised values are gathered on
+  // the device and written into the caller's row (hist_len pairs, not the row).
+  const bool pen = s->row_cfg[0].repeat_penalty != 1.0f && s->hist_maybe && s->hist_len > 0;
+  if (pen) {
+    if (s->pairs_cap < s->hist_len) {
+      HIP_TRY(s, hipStreamSynchronize(s->stream));
+      (void)hipFree(s->d_pairs);
+      if (s->h_pairs) (void)hipHostFree(s->h_pairs);
+      s->d_pairs = nullptr;
+      s->h_pairs = nullptr;
+      s->pairs_cap = 0;
+      HIP_TRY(s, hipMalloc(&s->d_pairs, sizeof(uint64_t) * (size_t)s->hist_len));
+      HIP_TRY(s, hipHostMalloc(&s->h_pairs, sizeof(uint64_t) * (size_t)s->hist_len, hipHostMallocDefault));
+      s->pairs_cap = s->hist_len;
+    }
+    HIP_TRY(s, launch_hist_gather(s->d_hist, s->hist_len, s->d_rows, s->d_row, vocab, s->d_pairs, s->stream));
+    HIP_TRY(s, hipMemcpyAsync(s->h_pairs, s->d_pairs, sizeof(uint64_t) * (size_t)s->hist_len,
                               hipMemcpyDeviceToHost, s->stream));
+  }
   HIP_TRY(s, hipStreamSynchronize(s->stream));
+  if (pen) {
+    for (int32_t j = 0; j < s->hist_len; ++j) {
+      const uint64_t e = s->h_pairs[j];
+      if (e == ~0ull) continue;
+      const uint32_t bits = (uint32_t)e;
+      memcpy(&logits[(uint32_t)(e >> 32)], &bits, sizeof(bits));
+    }
+  }
   return tok;
 }
 

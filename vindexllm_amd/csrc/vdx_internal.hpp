@@ -65,6 +65,8 @@ hipError_t launch_penalty(const CallParams &p, hipStream_t st);
 hipError_t launch_greedy(const CallParams &p, hipStream_t st);
 hipError_t launch_topk(const CallParams &p, hipStream_t st);
 hipError_t launch_full(const CallParams &p, hipStream_t st);
+hipError_t launch_hist_gather(const int32_t *hist_row, int32_t slots, const RowState *rs_row, const float *L,
+                              int32_t vocab, uint64_t *out, hipStream_t st);
 hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row0,
                            int32_t rows, int32_t *hist, int32_t hist_len,
                            RowState *rs, hipStream_t st);

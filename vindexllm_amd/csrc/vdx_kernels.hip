@@ -2091,6 +2091,25 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
 // =============================================================================
 // AddToHistory (Sampler.pas:530-539) for rows [row0, row0 + rows): the ring of
 // row r holds its own window's ids at hist + r * stride.
+// The history positions of one row after the penalty, for the host entry
+// point to mirror the in-place penalty into the caller's buffer: slot j < the
+// row's count holds id << 32 | bits(L[id]) for an in-range history id, every
+// other slot ~0.  Only history positions are ever penalised, so writing these
+// back reproduces the whole penalised row.
+__global__ void k_hist_gather(const int32_t *__restrict__ hist_row, int32_t slots,
+                              const RowState *__restrict__ rs_row, const float *__restrict__ L, int32_t vocab,
+                              uint64_t *__restrict__ out) {
+  const int cnt = min(rs_row->hist_count, slots);
+  for (int j = threadIdx.x; j < slots; j += blockDim.x) {
+    uint64_t e = ~0ull;
+    if (j < cnt) {
+      const int32_t id = hist_row[j];
+      if (id >= 0 && id < vocab) e = ((uint64_t)(uint32_t)id << 32) | __float_as_uint(L[id]);
+    }
+    out[j] = e;
+  }
+}
+
 __global__ void k_hist_add(const int32_t *__restrict__ tokens, int32_t tok_const, int32_t row0,
                            int32_t rows, int32_t *__restrict__ hist, int32_t stride,
                            RowState *__restrict__ rs) {
@@ -2194,6 +2213,12 @@ hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row
   const int nb = (rows + 255) / 256;
   hipLaunchKernelGGL(k_hist_add, dim3(nb), dim3(256), 0, st, tokens, tok_const, row0, rows, hist,
                      hist_len, rs);
+  return hipGetLastError();
+}
+
+hipError_t launch_hist_gather(const int32_t *hist_row, int32_t slots, const RowState *rs_row, const float *L,
+                              int32_t vocab, uint64_t *out, hipStream_t st) {
+  hipLaunchKernelGGL(k_hist_gather, dim3(1), dim3(256), 0, st, hist_row, slots, rs_row, L, vocab, out);
   return hipGetLastError();
 }
 

@@ -168,6 +168,13 @@ def load_library():
     if _lib is None:
         if not os.path.exists(_build.LIB):
             raise RuntimeError(f"{_build.LIB} is not built; run __graft_entry__.build()")
+        # One HIP runtime per process: where PyTorch is installed, its bundled
+        # libamdhip64 is loaded first, so the library binds to the same one
+        # (loading ROCm's first leaves torch's devices unavailable).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(_build.LIB)
         for name, (res, args) in _SIGNATURES.items():
             f = getattr(L, name)
