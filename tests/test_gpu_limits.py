@@ -2,7 +2,7 @@
 and just beyond it, against the oracle.
 
 At 256 chunks the top-K kernel's chunk quota is 8, so the stored candidates
-(>= 2048) exceed what the general merge holds in LDS and the rows are
+(>= 2048) can exceed what the general merge holds in LDS, and such rows are
 replayed (the reference's min-buffer scan, exact); the full and greedy
 kernels reduce 256 chunk records.  Bar: as the other parity tests
 (bit-exact tokens, index sets and penalised logits; probabilities within 1e-5
