@@ -46,6 +46,8 @@ sys.path.insert(0, ROOT)
 import numpy as np  # noqa: E402
 
 METRIC = "rows/sec sampled (B=64, V=262144, topk64/topp0.95); % of HBM peak"
+MIN_TIMED = 128          # fewest steps in a timed region
+NORTH_STAR = "topk_b256"  # B=256 top-k 64 / top-p 0.95: the >= 60% of HBM target
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 POOL_BYTES = 2 << 30
 
@@ -53,12 +55,11 @@ WORKLOADS = {
     "penalised_b64": dict(
         rows=64, vocab=262144, hist=256,
         cfg=dict(Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256, Seed=3003),
-        desc="penalised batch: B=64 V=262144 fp32 3*N(0,1)+6 at 32 hot ids/row, 256-id history/row, "
-             "RP 1.1 window 256, T 0.8, top-k 64, top-p 0.95"),
+        desc="penalised B=64 V=262144 3N(0,1)+6@32 ids, 256-id history, RP 1.1, T 0.8, top-k 64, top-p 0.95"),
     "topk_b256": dict(
         rows=256, vocab=262144, hist=0,
         cfg=dict(Temperature=1.0, TopK=64, TopP=0.95, Seed=3006),
-        desc="B=256 V=262144 fp32 3*N(0,1)+8 at 16 ids/row, T 1.0, top-k 64, top-p 0.95"),
+        desc="B=256 V=262144 3N(0,1)+8@16 ids, T 1.0, top-k 64, top-p 0.95"),
     "full_b256": dict(
         rows=256, vocab=262144, hist=0,
         cfg=dict(Temperature=0.7, TopK=0, TopP=0.9, Seed=3004),
@@ -77,9 +78,8 @@ WORKLOADS = {
                   dict(Temperature=0.7, TopK=40, TopP=0.9, MinP=0.05, RepeatPenalty=1.3,
                        RepeatWindow=128, Seed=3009),
                   dict(Temperature=1.0, TopK=0, RepeatPenalty=1.1, RepeatWindow=256, Seed=3010)],
-        desc="per-row configs: B=64 V=262144 as the penalised batch, rows cycling over "
-             "top-k 64/top-p 0.95 (RP 1.1), greedy (RP 1.2), top-k 40/top-p 0.9/min-p 0.05 "
-             "(RP 1.3) and full softmax T 1.0 (RP 1.1, separate penalty kernel)"),
+        desc="per-row configs B=64 V=262144, rows cycle top-k 64/top-p 0.95, greedy, "
+             "top-k 40/min-p 0.05, full softmax; all penalised"),
 }
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
@@ -199,7 +199,7 @@ def readback_cost(rows, vocab, reps=50):
     return out
 
 
-def run_gpu(name, steps, warmup, eager):
+def run_gpu(name, steps, warmup, eager, check=False):
     import torch
 
     from vindexllm_amd import TVdxSampler
@@ -228,23 +228,30 @@ def run_gpu(name, steps, warmup, eager):
             b.copy_(pristine)
         torch.cuda.synchronize()
 
-    graph = None
+    # The timed region runs exactly `steps` steps: steps // P replays of a
+    # graph over the whole pool, then one replay of a graph over the first
+    # steps % P buffers.
+    graph = rest = None
     if not eager:
-        g = torch.cuda.CUDAGraph()
         cs = torch.cuda.Stream(dev)
         cs.wait_stream(stream)
         with torch.cuda.stream(cs):
             s.process_device(pool[0], tokens=tok, stream=cs)  # workspace already sized
         torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=cs):
-            for i in range(P):
-                s.process_device(pool[i], tokens=tok, stream=cs)
-        torch.cuda.synchronize()
-        graph = g
-        reps = max(1, steps // P)
-        steps = reps * P
-        g.replay()
-        torch.cuda.synchronize()
+
+        def capture(n):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cs):
+                for i in range(n):
+                    s.process_device(pool[i], tokens=tok, stream=cs)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            return g
+
+        graph = capture(P)
+        if steps % P:
+            rest = capture(steps % P)
 
     restore()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -255,6 +262,8 @@ def run_gpu(name, steps, warmup, eager):
     if graph is not None:
         for _ in range(steps // P):
             graph.replay()
+        if rest is not None:
+            rest.replay()
     else:
         for i in range(steps):
             s.process_device(pool[i % P], tokens=tok, stream=stream)
@@ -274,11 +283,75 @@ def run_gpu(name, steps, warmup, eager):
     torch.cuda.synchronize()
     flags = fl.cpu().numpy()
     s.Free()
-    return dict(steps=steps, elapsed=elapsed, rows=B, vocab=V, step_bytes=step_bytes, pool=P,
-                kernel_ms=kernel_ms,
-                launch="hipGraph" if graph is not None else "eager",
-                fast_frac=float(((flags & 0x2) != 0).mean()),
-                replay_frac=float(((flags & 0x4) != 0).mean()))
+    out = dict(steps=steps, elapsed=elapsed, rows=B, vocab=V, step_bytes=step_bytes, pool=P,
+               kernel_ms=kernel_ms,
+               launch="hipGraph" if graph is not None else "eager",
+               fast_frac=float(((flags & 0x2) != 0).mean()),
+               replay_frac=float(((flags & 0x4) != 0).mean()))
+    if check:
+        out["parity"] = parity_check(name, L, hist)
+    return out
+
+
+def parity_check(name, L, hist, seed=4242):
+    """One sampling call on the workload's own pristine inputs with injected
+    per-row uniforms, outside any timed region, checked row by row against
+    the oracle (oracle/vdx_oracle.c): greedy and top-K tokens, top-K index
+    sets and penalised logits must be bit-exact; a full-softmax token may
+    differ only within 1e-6*S of a CDF boundary (counted)."""
+    import torch
+
+    from oracle import vdx_oracle as O
+    from vindexllm_amd import TVdxSampler
+
+    w = WORKLOADS[name]
+    B, V = L.shape
+    dev = torch.device("cuda:0")
+    u = (np.random.default_rng(seed).integers(0, 2**24, B) / 2**24).astype(np.float32)
+    d = torch.from_numpy(L).to(dev)
+    s = TVdxSampler(0, B)
+    configure(s, w)
+    if hist is not None:
+        for r in range(B):
+            s.set_history(r, hist[r][:max(s.GetRowConfig(r).RepeatWindow, 0)])
+    Kmax = max([w["cfg"].get("TopK", 0)] + [c.get("TopK", 0) for c in w.get("row_cfgs", [])] + [1])
+    ti = torch.full((B, Kmax), -1, dtype=torch.int32, device=dev)
+    fl = torch.zeros(B, dtype=torch.int32, device=dev)
+    tok = s.process_device(d, uniforms=torch.from_numpy(u).to(dev), topk_idx=ti, flags=fl)
+    torch.cuda.synchronize()
+    tok, ti, fl, after = tok.cpu().numpy(), ti.cpu().numpy(), fl.cpu().numpy(), d.cpu().numpy()
+    s.Free()
+    rc = w.get("row_cfgs")
+    mism = bnd = set_mism = logit_mism = 0
+    t0 = time.perf_counter()
+    for r in range(B):
+        c = rc[r % len(rc)] if rc else w["cfg"]
+        cfg = O.make_config(temperature=c.get("Temperature", 0.0), top_k=c.get("TopK", 0),
+                            top_p=c.get("TopP", 1.0), min_p=c.get("MinP", 0.0),
+                            repeat_penalty=c.get("RepeatPenalty", 1.0), repeat_window=c.get("RepeatWindow", 64))
+        row = L[r].copy()
+        h = hist[r][:max(c.get("RepeatWindow", 64), 0)] if hist is not None else None
+        want, tr = O.process_row(row, cfg, float(u[r]), hist=h, trace=True)
+        if not np.array_equal(row.view(np.uint32), after[r].view(np.uint32)):
+            logit_mism += 1
+        if tr.path == O.PATH_TOPK:
+            K = tr.k
+            order = sorted(range(K), key=lambda k: (-float(np.float32(tr.slot_val[k])), tr.slot_idx[k]))
+            if ti[r][:K].tolist() != [tr.slot_idx[k] for k in order]:
+                set_mism += 1
+        if tok[r] != want:
+            dist = (min(tr.target - tr.cdf_lo, tr.cdf_hi - tr.target) / tr.sum_final
+                    if tr.sum_final > 0 and np.isfinite(tr.sum_final) else np.inf)
+            if tr.path == O.PATH_FULL and dist < 1e-6:
+                bnd += 1
+            else:
+                mism += 1
+    return {"rows": B, "token_mismatches": mism, "boundary_draws": bnd, "topk_set_mismatches": set_mism,
+            "penalised_logit_mismatches": logit_mism,
+            "rows_fast_path": int(((fl & 0x2) != 0).sum()), "rows_replay_path": int(((fl & 0x4) != 0).sum()),
+            "oracle_s": round(time.perf_counter() - t0, 3),
+            "bar": "tokens/top-K sets/penalised logits bit-exact; full-path draws within 1e-6*S of a "
+                   "boundary counted"}
 
 
 LMHEAD_V, LMHEAD_D = 262144, 2560  # Gemma-3-4B tied lm_head (token_embd.weight)
@@ -435,7 +508,7 @@ def copy_calibration(nbytes=1 << 30, reps=5):
 
 PMC_COMMAND = ("timeout -s KILL 60 rocprofv3 --pmc {counter} -f csv -d gpurun_out/pmc_{tag}_{workload} -o {tag} -- "
                "python -u bench.py --workload {workload} --eager --steps 20 --warmup 3 --no-cpu "
-               "--copy-calibration")
+               "--no-check --no-north-star --copy-calibration")
 
 
 def _kernel_base(name):
@@ -505,6 +578,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="issue every step from Python")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true", help="skip the oracle parity check of the inputs")
+    ap.add_argument("--no-north-star", action="store_true", help="skip the B=256 north-star workload")
     ap.add_argument("--others", action="store_true", help="also measure the other workloads")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--lmhead", type=int, metavar="B",
@@ -531,7 +606,10 @@ def main():
         if a.copy_calibration:
             copy_calibration()
         return
-    r = run_gpu(a.workload, a.steps, a.warmup, a.eager)
+    # at least MIN_TIMED steps are timed (a few hundred microseconds of work
+    # is too short a region to be stable); "steps" reports the count timed
+    steps = max(a.steps, MIN_TIMED)
+    r = run_gpu(a.workload, steps, a.warmup, a.eager, check=not a.no_check)
     rows_s = r["rows"] * r["steps"] / r["elapsed"]
     ms_step = 1e3 * r["elapsed"] / r["steps"]
     achieved = r["step_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
@@ -541,6 +619,7 @@ def main():
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": r["steps"],
+        "steps_requested": a.steps,
         "warmup": a.warmup,
         "ms_per_step": ms_step,
         "higher_is_better": True,
@@ -560,6 +639,18 @@ def main():
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(a.workload),
                      "kernel_us": 1e3 * r["kernel_ms"], "bytes_per_launch": r["step_bytes"]},
     }
+    if "parity" in r:
+        out["parity"] = r["parity"]
+    if NORTH_STAR != a.workload and not a.no_north_star:
+        # the target shape: B=256 x V=262144 fp32, top-k 64 / top-p 0.95
+        n = run_gpu(NORTH_STAR, steps, min(a.warmup, 20), a.eager, check=not a.no_check)
+        nb = n["step_bytes"] / (n["kernel_ms"] * 1e-3) / 1e9
+        out["north_star"] = {"workload": WORKLOADS[NORTH_STAR]["desc"], "steps": n["steps"],
+                             "rows_per_s": n["rows"] * n["steps"] / n["elapsed"],
+                             "us_per_step": 1e6 * n["elapsed"] / n["steps"],
+                             "kernel_us": 1e3 * n["kernel_ms"], "achieved_GBs": nb,
+                             "hbm_frac": nb / HBM_PEAK_GBS, "target_frac": 0.60,
+                             "rows_fast_path": n["fast_frac"], "parity": n.get("parity")}
     if a.others:
         others = {}
         for name in WORKLOADS:

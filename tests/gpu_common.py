@@ -1,8 +1,8 @@
 """Shared helpers of the GPU parity tests: run the HIP sampler and the CPU
 oracle on the same seeded inputs and compare them to the parity bar:
-tokens identical except draws within 1e-6*S of a CDF boundary (counted),
-top-K index sets and penalised logits bit-exact, probabilities within 1e-5
-relative."""
+full-softmax tokens identical except draws within 1e-6*S of a CDF boundary
+(counted), greedy and top-K tokens, top-K index sets and penalised logits
+bit-exact, probabilities within 1e-5 relative."""
 from __future__ import annotations
 
 import sys
@@ -119,9 +119,14 @@ def compare(g, orc, cfg, check_topk=True, check_logits=True, label=""):
             assert np.array_equal(g["logits_after"][r].view(np.uint32), row.view(np.uint32)), \
                 f"{label} row {r}: penalised logits differ"
         if g["tokens"][r] != tok:
+            # Only the full-softmax path may differ, and only within 1e-6*S of a
+            # CDF boundary: its chunked fp64 sums are associated differently
+            # from the reference's index-order sum.  Top-K and greedy rows
+            # reproduce the reference's sums and order bit for bit.
             d = boundary_distance(tr)
-            assert d < BOUNDARY_EPS, (f"{label} row {r}: token {g['tokens'][r]} != oracle {tok} "
-                                      f"(boundary distance {d:.3e}, flags {g['flags'][r]:#x})")
+            assert tr.path == O.PATH_FULL and d < BOUNDARY_EPS, (
+                f"{label} row {r}: token {g['tokens'][r]} != oracle {tok} (path {tr.path}, "
+                f"boundary distance {d:.3e}, flags {g['flags'][r]:#x})")
             n_boundary += 1
         if check_topk and tr.path == O.PATH_TOPK and g["topk_idx"] is not None:
             idx, prob = canonical_topk(tr)

@@ -488,3 +488,54 @@ def test_graph_replay_matches_eager():
             assert torch.equal(tok, eager), rep
             assert torch.equal(buf, eager_logits), rep
             _ = (pristine * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_graph_captured_with_empty_rings_applies_penalty():
+    # A decode step [sample, append the token to the ring] captured while every
+    # ring is empty, then replayed: from the second replay on the rings hold
+    # ids and the penalty must apply, exactly as eager calls apply it.
+    import torch
+    from vindexllm_amd import TVdxSampler
+
+    log("[case] graph captured with empty rings")
+    rng = np.random.default_rng(57)
+    B, V = 8, 20000
+    L = (2.0 * rng.standard_normal((B, V))).astype(np.float32)
+    for r in range(B):
+        L[r, rng.choice(V, 6, replace=False)] += np.float32(6.0)
+    u = torch.from_numpy(u_stream(rng, B)).cuda()
+    pristine = torch.from_numpy(L).cuda()
+    kw = dict(Temperature=1.0, TopK=8, TopP=0.9, RepeatPenalty=3.0, RepeatWindow=16, Seed=3)
+    with TVdxSampler(0, B) as s, TVdxSampler(0, B) as ref:
+        _cfg(s, **kw)
+        _cfg(ref, **kw)
+        buf = pristine.clone()
+        tok = torch.zeros(B, dtype=torch.int32, device="cuda")
+        # one eager call sizes the workspace for V (a call under capture must
+        # not allocate); with empty rings and an injected uniform it changes
+        # no state
+        s.process_device(pristine.clone(), uniforms=u)
+        torch.cuda.synchronize()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            s.process_device(buf, uniforms=u, tokens=tok, stream=cs)
+            s.add_to_history_device(tok, stream=cs)
+        torch.cuda.synchronize()
+        seen_penalty = False
+        for step in range(5):
+            buf.copy_(pristine)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            rbuf = pristine.clone()
+            rtok = ref.process_device(rbuf, uniforms=u)
+            ref.add_to_history_device(rtok)
+            torch.cuda.synchronize()
+            assert torch.equal(tok, rtok), (step, tok, rtok)
+            assert torch.equal(buf, rbuf), step
+            seen_penalty = seen_penalty or not torch.equal(buf, pristine)
+            _ = (pristine * 2).sum().item()  # unrelated eager work between replays
+        assert seen_penalty
+    log("[done] graph captured with empty rings")

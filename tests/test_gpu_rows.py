@@ -180,7 +180,12 @@ def test_row_checkpoint_restores_the_stream():
             _set(s, 3, dict(temperature=1.3, min_p=0.02, seed=11, repeat_penalty=1.1, repeat_window=4))
             run(s, ident, 0, 6)
             blobs = s.save_state()
-            want = run(s, ident, 6, 14)
+            want = run(s, ident, 6, 10)
+            # ResetHistory reseeds every row with Seed > 0 (Sampler.pas:541-549):
+            # a restored row must restart the stream it was taken from, for
+            # both generators (the Philox key and counter row included)
+            s.ResetHistory(-1)
+            want = np.concatenate([want, run(s, ident, 10, 14)])
             cfg1 = s.GetRowConfig(1)
         perm = np.array([3, 0, 4, 1, 2])  # new row j holds saved row perm[j]
         with TVdxSampler(0, B + 2) as s2:
@@ -189,7 +194,9 @@ def test_row_checkpoint_restores_the_stream():
             for j in range(B):
                 s2.load_row_state(j, blobs[perm[j]])
             assert s2.GetRowConfig(3).TopK == cfg1.TopK and s2.GetRowConfig(3).Seed == 9
-            got = run(s2, perm, 6, 14)
+            got = run(s2, perm, 6, 10)
+            s2.ResetHistory(-1)
+            got = np.concatenate([got, run(s2, perm, 10, 14)])
         assert np.array_equal(got, want[:, perm]), (kind, got, want[:, perm])
         log(f"[done] row checkpoints kind={kind}")
 
@@ -218,6 +225,27 @@ def test_set_config_takes_every_row_back():
         first = [O.lib().vdxo_u24(O.xoshiro_stream(O.seed_state(21 + r), 1)[0]) for r in range(B)]
         assert uo.cpu().numpy()[1] == np.float32(first[1])
     log("[done] set_config after row configs")
+
+
+def test_set_config_same_window_keeps_history():
+    # After per-row configs widened the ring stride, a SetConfig that changes
+    # only the temperature keeps every row's history: the reference clears it
+    # only when RepeatWindow changes (Sampler.pas:137-142).
+    from vindexllm_amd import TVdxSampler
+
+    log("[case] set_config with an unchanged window")
+    with TVdxSampler(0, 2) as s:
+        _set(s, None, dict(temperature=1.0, seed=4, repeat_window=8))
+        _set(s, 1, dict(temperature=1.0, seed=4, repeat_window=16))
+        _set(s, None, dict(temperature=1.0, seed=4, repeat_window=8))
+        for r in range(2):
+            for t in (r + 5, r + 6, r + 7):
+                s.AddToHistory(t, row=r)
+        _set(s, None, dict(temperature=0.6, seed=4, repeat_window=8))
+        assert [s.get_history(r)[0] for r in range(2)] == [[5, 6, 7], [6, 7, 8]]
+        _set(s, None, dict(temperature=0.6, seed=4, repeat_window=9))  # a new window clears
+        assert [s.get_history(r)[0] for r in range(2)] == [[], []]
+    log("[done] set_config with an unchanged window")
 
 
 def test_load_row_state_rejects_bad_blobs():

@@ -225,6 +225,66 @@ def test_topk_uniform_closed_form():
         assert tok == int(np.floor(np.float64(np.float32(u)) * K))
 
 
+@pytest.mark.parametrize("top_p", [0.5, 0.25, 0.95, 0.3, 0.999, 1e-9])
+def test_topk_top_p_uniform_closed_form(top_p):
+    # Equal logits: slots hold 0..K-1, every q = 1, S = K.  The stable sort
+    # keeps slot order; the cut keeps q while C < target = TopP * K, i.e. the
+    # n = ceil(target) entries C = 0 .. n-1 (the crossing entry included);
+    # S' = n and the draw returns floor(u * n).  "C <= target", dropping the
+    # crossing entry, or a target on S' instead of S all fail here.
+    K, V = 64, 700
+    L = np.full(V, -1.75, dtype=np.float32)
+    target = np.float64(np.float32(top_p)) * K
+    n = int(np.ceil(target))
+    for k in range(0, 2**24, 2**24 // 61):
+        u = k / 2**24
+        tok, tr = O.process_row(L.copy(), O.make_config(temperature=0.9, top_k=K, top_p=top_p), u, trace=True)
+        assert tr.sum_final == n
+        assert tok == int(np.floor(np.float64(np.float32(u)) * n)), (top_p, u)
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.6])
+def test_topk_min_p_two_level_closed_form(top_p):
+    # K = 64 slots over a row of zeros with 10 logits of 5.0 at indices >= K:
+    # each 5.0 enters and evicts the first strict-minimum slot, so they take
+    # slots 0..9 in index order; slots 10..63 keep indices 10..63 (value 0).
+    # q = 1 for the 5.0 entries, qB = fl32(exp(-5 invT)) for the rest.
+    K, V, T = 64, 5000, 1.25
+    rng = np.random.default_rng(31)
+    hot = np.sort(rng.choice(np.arange(K, V), 10, replace=False))
+    L = np.zeros(V, dtype=np.float32)
+    L[hot] = 5.0
+    inv_t = np.float32(np.float32(1.0) / np.float32(T))
+    qb = np.float32(np.exp(np.float64(-5.0) * np.float64(inv_t)))
+    us = [k / 2**24 for k in range(0, 2**24, 2**24 // 53)] + [1 - 2**-24]
+    # (a) MinP above qB: every q < thr = fl32(1 * MinP) is zeroed, S = 10;
+    #     Top-P keeps n = ceil(TopP * 10) of the equal q in slot order
+    n = int(np.ceil(np.float64(np.float32(top_p)) * 10))
+    for u in us:
+        tok = O.process_row(L.copy(), O.make_config(temperature=T, top_k=K, top_p=top_p,
+                                                    min_p=float(qb) * 1.5), u)
+        assert tok == hot[int(np.floor(np.float64(np.float32(u)) * n))], u
+    # (b) MinP = qB exactly: q < thr is strict, so nothing is zeroed and
+    #     S = 10 + 54 qB exactly (every partial sum fits in 53 bits); with
+    #     TopP = 1 the draw walks the slots: hot[floor(t)] while t < 10,
+    #     else index 10 + j for the first j with 10 + (j + 1) qB > t
+    if top_p == 1.0:
+        S = 10.0 + 54.0 * np.float64(qb)
+        for u in us:
+            tok, tr = O.process_row(L.copy(), O.make_config(temperature=T, top_k=K, min_p=float(qb)), u,
+                                    trace=True)
+            assert tr.sum_final == S
+            t = np.float64(np.float32(u)) * S
+            if t < 10.0:
+                want = hot[int(np.floor(t))]
+            else:
+                j = 0
+                while not (10.0 + (j + 1) * np.float64(qb) > t):
+                    j += 1
+                want = 10 + j
+            assert tok == want, u
+
+
 # ------------------------------------------------------------ full path ----
 @pytest.mark.parametrize("min_p,T", [(0.0, 1.0), (0.0, 0.7), (0.05, 1.3)])
 def test_full_path_matches_restatement(min_p, T):

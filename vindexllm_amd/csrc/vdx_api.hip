@@ -23,7 +23,7 @@ struct vdx_sampler {
   vdx_sampler_config cfg{};
   int32_t rng_kind = VDX_RNG_XOSHIRO;
   uint64_t seed_base = 0;  // resolved seed: Seed, or a timer value when Seed = 0
-  bool hist_maybe = false; // some row may hold history ids
+  bool hist_maybe = false; // some row may hold history ids (host Process write-back)
   hipStream_t stream = nullptr;
   RowState *d_rows = nullptr;
   int32_t *d_hist = nullptr;
@@ -32,7 +32,9 @@ struct vdx_sampler {
   bool per_row = false;
   std::vector<vdx_sampler_config> row_cfg;  // every row's config (= cfg without per-row configs)
   std::vector<uint8_t> own_seed;            // row seeded from its own Seed (else seed_base + row)
-  std::vector<uint64_t> own_seed_val;       // that seed, resolved (timer value for Seed = 0)
+  std::vector<uint64_t> own_seed_val;       // that seed, resolved (timer value for Seed = 0): the xoshiro seed
+  std::vector<uint64_t> own_pkey;           // the row's Philox key (its own seed, or a restored stream's)
+  std::vector<int32_t> own_prow;            // the row's Philox counter row (-1: the row itself)
   RowCfg *d_rcfg = nullptr;
   // a call whose rows take several paths runs their kernels side by side:
   // forked onto these streams after the penalty, joined before returning
@@ -94,12 +96,16 @@ static uint64_t timer_seed() {
 
 static int32_t chunks_for(int32_t vocab) { return (vocab + kChunk - 1) / kChunk; }
 
-// Reseeds row `row` the way its config says: from its own resolved Seed, or
-// as row `row` of the sampler-wide config (seed_base + row).
+// Reseeds row `row` the way its config says: from its own resolved Seed (or
+// the stream a restored checkpoint was taken from), or as row `row` of the
+// sampler-wide config (xoshiro from seed_base + row, Philox keyed by seed_base).
 static int reseed_row(vdx_sampler *s, int32_t row) {
-  const bool own = s->own_seed[row] != 0;
-  HIP_TRY(s, launch_row_reset(s->d_rows, row, 1, false, -1, true, own ? s->own_seed_val[row] : s->seed_base,
-                              !own, s->stream));
+  if (s->own_seed[row])
+    HIP_TRY(s, launch_row_reset(s->d_rows, row, 1, false, -1, true, s->own_seed_val[row], false, s->stream,
+                                s->own_pkey[row], s->own_prow[row]));
+  else
+    HIP_TRY(s, launch_row_reset(s->d_rows, row, 1, false, -1, true, s->seed_base, true, s->stream,
+                                s->seed_base, -1));
   return VDX_OK;
 }
 
@@ -107,7 +113,8 @@ static int reseed_row(vdx_sampler *s, int32_t row) {
 // or a row's own Seed.
 static int reseed_all(vdx_sampler *s) {
   s->seed_base = (s->cfg.seed == 0) ? timer_seed() : (uint64_t)s->cfg.seed;
-  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, false, -1, true, s->seed_base, true, s->stream));
+  HIP_TRY(s, launch_row_reset(s->d_rows, 0, s->max_rows, false, -1, true, s->seed_base, true, s->stream,
+                              s->seed_base, -1));
   for (int32_t r = 0; r < s->max_rows; ++r)
     if (s->own_seed[r]) {
       int rc = reseed_row(s, r);
@@ -283,6 +290,8 @@ int vdx_sampler_create(vdx_sampler **out, int32_t device, int32_t max_rows) {
   s->row_cfg.assign((size_t)max_rows, s->cfg);
   s->own_seed.assign((size_t)max_rows, 0);
   s->own_seed_val.assign((size_t)max_rows, 0);
+  s->own_pkey.assign((size_t)max_rows, 0);
+  s->own_prow.assign((size_t)max_rows, -1);
   int rc = VDX_OK;
   do {
     if ((e = hipSetDevice(device)) != hipSuccess) { rc = hip_fail(s, e, "hipSetDevice"); break; }
@@ -334,7 +343,9 @@ int vdx_sampler_set_config(vdx_sampler *s, const vdx_sampler_config *c) {
   const int32_t want = window_of(*c);
   int rc = VDX_OK;
   if (!s->per_row) {
-    if (want != s->hist_len && (rc = alloc_history(s, want)) != VDX_OK) return rc;
+    // a RepeatWindow change resizes and clears the history (Sampler.pas:137-142);
+    // the ring stride may exceed the window (widened by earlier per-row configs)
+    if (want != window_of(s->cfg) && (rc = alloc_history(s, want)) != VDX_OK) return rc;
   } else {
     // every row takes the sampler-wide config again: rows whose window
     // changes lose their history, rows with their own seed are reseeded
@@ -386,6 +397,8 @@ int vdx_sampler_set_row_config(vdx_sampler *s, int32_t row, const vdx_sampler_co
   if (old.seed != c->seed) {  // a new Seed reseeds the row from it (Sampler.pas:144-150)
     s->own_seed[row] = 1;
     s->own_seed_val[row] = c->seed == 0 ? timer_seed() : (uint64_t)c->seed;
+    s->own_pkey[row] = s->own_seed_val[row];
+    s->own_prow[row] = -1;
     if ((rc = reseed_row(s, row)) != VDX_OK) return rc;
   }
   HIP_TRY(s, hipStreamSynchronize(s->stream));
@@ -482,8 +495,10 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
 
   // Step 0: repetition penalty (Sampler.pas:287); the sampling kernels apply
   // it themselves for windows of up to kPenMax ids; otherwise a separate
-  // kernel runs first (for the rows that need it)
-  const bool hist = s->hist_maybe && s->hist_len > 0;
+  // kernel runs first (for the rows that need it).  Whether it runs depends
+  // on the configs only (each kernel reads the row's ring count and skips an
+  // empty ring), so a captured call applies it once the device fills rings.
+  const bool hist = s->hist_len > 0;
   p.fuse_penalty = (hist && pen_fused) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
@@ -765,7 +780,8 @@ int vdx_sampler_reset_history(vdx_sampler *s, int32_t row) {
   // ResetHistory (Sampler.pas:541-549): reseed only when Seed > 0
   if (!s->per_row) {
     const bool reseed = s->cfg.seed > 0;
-    HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, -1, reseed, s->seed_base, true, s->stream));
+    HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, -1, reseed, s->seed_base, true, s->stream,
+                                s->seed_base, -1));
   } else {
     HIP_TRY(s, launch_row_reset(s->d_rows, r0, n, true, -1, false, 0, false, s->stream));
     for (int32_t r = r0; r < r0 + n; ++r)
@@ -874,8 +890,11 @@ int vdx_sampler_load_row_state(vdx_sampler *s, int32_t row, const void *buf, int
   s->per_row = true;
   // the restored state carries its own seed: later reseeds of this row
   // (ResetHistory with Seed > 0, set_rng) start the stream it was taken from
+  // (xoshiro from its seed; Philox under its key and counter row)
   s->own_seed[row] = 1;
   s->own_seed_val[row] = h.own_seed_val;
+  s->own_pkey[row] = h.state.key;
+  s->own_prow[row] = h.state.ctr_row;
   HIP_TRY(s, hipMemcpy(s->d_rows + row, &h.state, sizeof(RowState), hipMemcpyHostToDevice));
   if (w > 0)
     HIP_TRY(s, hipMemcpy(s->d_hist + (int64_t)row * s->hist_len, (const char *)buf + sizeof(h),

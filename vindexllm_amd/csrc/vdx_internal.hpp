@@ -70,7 +70,10 @@ hipError_t launch_hist_gather(const int32_t *hist_row, int32_t slots, const RowS
 hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row0,
                            int32_t rows, int32_t *hist, int32_t hist_len,
                            RowState *rs, hipStream_t st);
+// Reseeding: xoshiro from seed (+ row when add_row); Philox keyed by pkey,
+// counting on prow (< 0: the row itself).
 hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, int32_t window,
-                            bool reseed, uint64_t seed, bool add_row, hipStream_t st);
+                            bool reseed, uint64_t seed, bool add_row, hipStream_t st, uint64_t pkey = 0,
+                            int32_t prow = -1);
 
 }  // namespace vdx

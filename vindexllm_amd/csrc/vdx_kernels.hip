@@ -1387,12 +1387,20 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
           S = S + (double)sm.q[k];
       }
     }
-    // Top-P (:431-444)
+    // Top-P (:431-444).  S was summed in value order; the reference sums in
+    // slot order.  Each order's rounded sum of K non-negative terms is within
+    // (K-1) 2^-53 S of the exact sum, so the two targets differ by at most
+    // tol; a running sum C (summed in the draw order, as the reference does)
+    // within tol of the target could fall on either side of the reference's:
+    // such rows take the exact path.
     const double target = (double)p.top_p * S;
+    const double tol = (double)p.top_p * (double)(2 * K) * 0x1p-53 * S + 0x1p-51 * target;
+    bool near_cut = false;
     double C = 0.0, S2 = 0.0;
     int cut = K;
     for (int k = 0; k < K; ++k) {
       const float qk = sm.q[k];
+      if (qk > 0.0f && fabs(C - target) <= tol) near_cut = true;
       if (C < target && qk > 0.0f) {
         C = C + (double)qk;
         S2 = S2 + (double)qk;
@@ -1402,7 +1410,7 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
         sm.q_ord[k] = 0.0f;
       }
     }
-    bool amb = (cut > 0 && cut < K) && sm.q[cut] > 0.0f && sm.q[cut] == sm.q[cut - 1];
+    bool amb = near_cut || ((cut > 0 && cut < K) && sm.q[cut] > 0.0f && sm.q[cut] == sm.q[cut - 1]);
     // draw (:447-459)
     const double t = (double)sm.uval * S2;
     C = 0.0;
@@ -2134,12 +2142,14 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t &s) {
 }
 
 // Clears the rings of rows [row0, row0 + rows) (and sets their window when
-// window >= 0) and/or reseeds them (SeedPRNG, Sampler.pas:224-241): with
-// seed + row (rows of the sampler-wide config behave as samplers with Seed +
-// r), or with `seed` itself (a row with its own config).  The Philox stream
-// of a row is keyed by `seed` and counts on (step, row).
+// window >= 0) and/or reseeds them (SeedPRNG, Sampler.pas:224-241): xoshiro
+// from seed + row (rows of the sampler-wide config behave as samplers with
+// Seed + r), or from `seed` itself (a row with its own config or a restored
+// checkpoint).  The Philox stream of a row is keyed by `pkey` and counts on
+// (step, prow), prow < 0 standing for the row itself.
 __global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t rows, int clear_hist,
-                            int32_t window, int reseed, uint64_t seed, int add_row) {
+                            int32_t window, int reseed, uint64_t seed, int add_row, uint64_t pkey,
+                            int32_t prow) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   const int row = row0 + r;
@@ -2151,8 +2161,8 @@ __global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t row
   }
   if (reseed) {
     uint64_t st = seed + (add_row ? (uint64_t)row : 0ull);
-    s.key = seed;
-    s.ctr_row = row;
+    s.key = pkey;
+    s.ctr_row = prow < 0 ? row : prow;
     s.rng[0] = splitmix64(st);
     s.rng[1] = splitmix64(st);
     s.rng[2] = splitmix64(st);
@@ -2223,10 +2233,11 @@ hipError_t launch_hist_gather(const int32_t *hist_row, int32_t slots, const RowS
 }
 
 hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, int32_t window,
-                            bool reseed, uint64_t seed, bool add_row, hipStream_t st) {
+                            bool reseed, uint64_t seed, bool add_row, hipStream_t st, uint64_t pkey,
+                            int32_t prow) {
   const int nb = (rows + 255) / 256;
   hipLaunchKernelGGL(k_row_reset, dim3(nb), dim3(256), 0, st, rs, row0, rows, clear_hist ? 1 : 0,
-                     window, reseed ? 1 : 0, seed, add_row ? 1 : 0);
+                     window, reseed ? 1 : 0, seed, add_row ? 1 : 0, pkey, prow);
   return hipGetLastError();
 }
 
