@@ -120,6 +120,33 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows,
                                const float *uniforms,
                                const vdx_sample_outputs *out, void *stream);
 
+/* Allocation-free sampling.  No counterpart in the reference: this entry
+ * point is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It
+ * needs no sampler object and calls no hipMalloc, hipFree or allocating
+ * library routine: its workspace is a fixed device array inside the library
+ * (about 4.4 MiB per device, held until the process ends), whose device
+ * address is looked up once per device on the first call made with that
+ * device current.
+ *
+ * It samples `rows` device-resident rows exactly as vdx_sampler_process_device
+ * does for a sampler whose config is *cfg, whose row r holds the ring of
+ * history_count[r] ids at history + r*history_stride (the repetition penalty
+ * is applied in place, as Sampler.pas:285-303 does; a count is clamped to
+ * [0, min(RepeatWindow, history_stride)]), and whose draws are the injected
+ * `uniforms` (device, one per row, required: there is no RNG state).
+ * history/history_count may be NULL (no penalty).  Limits: rows <= 1024 and
+ * rows * ceil(vocab / 16384) <= 4096 (e.g. 256 rows of 262144 logits), else
+ * VDX_E_UNSUPPORTED.  Every call on one device shares that workspace and
+ * overwrites it: calls that overlap on one device (concurrent streams or
+ * threads) race and must be serialised by the caller.  Stream-ordered,
+ * asynchronous; the message of a failure is vdx_sampler_last_error(NULL). */
+int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int32_t rows,
+                              int32_t vocab, int64_t row_stride, const float *uniforms,
+                              const int32_t *history, int32_t history_stride,
+                              const int32_t *history_count, const vdx_sample_outputs *out,
+                              void *stream);
+
 /* The Q4_0 lm_head alone: shaders/matvec_q4_0.comp as
  * TVdxAttention.DispatchMatVec issues it for ATensorType = gtQ4_0
  * (Attention.pas:979-1025) from TVdxModel.UnembedToLogits (Model.pas:1258-1270),

@@ -9,6 +9,7 @@
 #include <string.h>
 #include <time.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -217,6 +218,53 @@ static int ensure_workspace(vdx_sampler *s, int32_t vocab) {
   // every record is written by its chunk before the row's last workgroup reads it
   s->ws_chunks = S;
   return VDX_OK;
+}
+
+// ---- allocation-free sampling ------------------------------------------------
+// vdx_sample_device_noalloc keeps its workspace (row states, arrival tickets,
+// chunk records, candidate slots) in one file-scope device array instead of
+// memory the library allocates.  In host code the array's name is only a
+// stand-in: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and that address is what
+// the kernels receive.  Every call on a device shares the device's copy.
+constexpr int32_t kNoAllocRows = 1024;        // rows per call
+constexpr int32_t kNoAllocRowChunks = 4096;   // rows * ceil(vocab / 16384) per call
+constexpr size_t na_align(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kNaRows = 0;
+constexpr size_t kNaTickets = kNaRows + na_align(sizeof(RowState) * kNoAllocRows);
+constexpr size_t kNaMeta = kNaTickets + na_align(sizeof(uint32_t) * kNoAllocRows);
+constexpr size_t kNaCand = kNaMeta + na_align(sizeof(ChunkMeta) * kNoAllocRowChunks);
+constexpr size_t kNaFullMeta = kNaCand + na_align(sizeof(Cand) * kCandCap * kNoAllocRowChunks);
+constexpr size_t kNaGpart = kNaFullMeta + na_align(sizeof(FullMeta) * kNoAllocRowChunks);
+constexpr size_t kNoAllocBytes = kNaGpart + na_align(sizeof(uint64_t) * kNoAllocRowChunks);
+static_assert(kNoAllocBytes <= (size_t)5 << 20, "the allocation-free workspace stays under 5 MiB per device");
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static unsigned char *g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// The device address of the current device's `scratch` (looked up on the
+// first call on that device); nullptr with the message in g_call_err.
+static unsigned char *scratch_on_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    g_call_err = std::string("noalloc: no current HIP device (") + hipGetErrorString(e) + ")";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    unsigned char *ptr = nullptr;
+    e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      g_call_err = std::string("noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
 }
 
 extern "C" {
@@ -531,6 +579,78 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
     HIP_TRY(s, hipEventRecord(ev[2], st));
     ++s->n_timed;
   }
+  return VDX_OK;
+}
+
+int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int32_t rows, int32_t vocab,
+                              int64_t row_stride, const float *uniforms, const int32_t *history,
+                              int32_t history_stride, const int32_t *history_count,
+                              const vdx_sample_outputs *out, void *stream) {
+  auto bad = [](int code, const char *m) {
+    g_call_err = m;
+    return code;
+  };
+  if (!cfg || !logits || !uniforms || !out || !out->tokens)
+    return bad(VDX_E_INVALID_ARG, "noalloc: cfg, logits, uniforms and out->tokens are required");
+  if (rows <= 0 || vocab <= 0 || row_stride < vocab)
+    return bad(VDX_E_INVALID_ARG, "noalloc: need rows > 0, vocab > 0 and row_stride >= vocab");
+  const RowCfg rc = row_params(*cfg);
+  const int path = row_path(rc, vocab);
+  const int32_t S = chunks_for(vocab);
+  if (rows > kNoAllocRows || (int64_t)rows * S > kNoAllocRowChunks)
+    return bad(VDX_E_UNSUPPORTED, "noalloc: rows * ceil(vocab / 16384) must be <= 4096 and rows <= 1024 "
+                                  "(the fixed workspace)");
+  if (S > kMaxChunks) return bad(VDX_E_UNSUPPORTED, "noalloc: vocab > 4194304 is not supported");
+  if (path == 1 && rc.top_k > kKMax) return bad(VDX_E_UNSUPPORTED, "noalloc: TopK > 64 is not implemented");
+  if ((out->topk_idx || out->topk_prob) && path == 1 && out->topk_stride < rc.top_k)
+    return bad(VDX_E_INVALID_ARG, "noalloc: topk_stride must be >= TopK");
+  const int32_t window = rc.window;
+  const bool pen = rc.penalty != 1.0f && window > 0 && history != nullptr;
+  if (pen && history_stride <= 0) return bad(VDX_E_INVALID_ARG, "noalloc: history_stride must be > 0");
+  unsigned char *ws = scratch_on_current_device();
+  if (!ws) return VDX_E_HIP;
+  hipStream_t st = (hipStream_t)stream;
+
+  CallParams p{};
+  p.logits = logits;
+  p.stride = row_stride;
+  p.rows = rows;
+  p.vocab = vocab;
+  p.nchunks = S;
+  p.vec = ((uintptr_t)logits % 16 == 0) && (row_stride % 4 == 0) && (vocab % 4 == 0);
+  p.inv_t = rc.inv_t;
+  p.top_k = rc.top_k;
+  p.top_p = rc.top_p;
+  p.min_p = rc.min_p;
+  p.penalty = rc.penalty;
+  p.hist = pen ? history : nullptr;
+  p.hist_len = pen ? history_stride : 0;
+  p.fuse_penalty = (pen && row_fuses_penalty(rc, vocab)) ? 1 : 0;
+  p.rcfg = nullptr;
+  p.rng.uniforms = uniforms;
+  p.rng.rows = reinterpret_cast<RowState *>(ws + kNaRows);
+  p.rng.kind = VDX_RNG_XOSHIRO;
+  p.rng.u_out = out->uniforms;
+  p.out.tokens = out->tokens;
+  p.out.topk_idx = path == 1 ? out->topk_idx : nullptr;
+  p.out.topk_prob = path == 1 ? out->topk_prob : nullptr;
+  p.out.topk_stride = out->topk_stride;
+  p.out.flags = out->flags;
+  p.meta = reinterpret_cast<ChunkMeta *>(ws + kNaMeta);
+  p.cand = reinterpret_cast<Cand *>(ws + kNaCand);
+  p.fmeta = reinterpret_cast<FullMeta *>(ws + kNaFullMeta);
+  p.gpart = reinterpret_cast<uint64_t *>(ws + kNaGpart);
+  p.tickets = reinterpret_cast<uint32_t *>(ws + kNaTickets);
+  // a row's count is clamped to its window and to the row's stride
+  hipError_t e = launch_rows_prepare(p.rng.rows, p.tickets, rows, pen ? history_count : nullptr,
+                                     pen ? (window < history_stride ? window : history_stride) : 0, st);
+  if (e == hipSuccess && pen && !p.fuse_penalty) e = launch_penalty(p, st);
+  if (e == hipSuccess) e = path == 0 ? launch_greedy(p, st) : (path == 1 ? launch_topk(p, st) : launch_full(p, st));
+  if (e != hipSuccess) {
+    g_call_err = std::string("noalloc launch: ") + hipGetErrorString(e);
+    return VDX_E_HIP;
+  }
+  g_call_err.clear();
   return VDX_OK;
 }
 

@@ -75,5 +75,9 @@ hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row
 hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear_hist, int32_t window,
                             bool reseed, uint64_t seed, bool add_row, hipStream_t st, uint64_t pkey = 0,
                             int32_t prow = -1);
+// RowState and tickets of rows [0, rows) for a call without a sampler object:
+// history counts from `count` (nullable: empty rings), tickets cleared.
+hipError_t launch_rows_prepare(RowState *rs, uint32_t *tickets, int32_t rows, const int32_t *count,
+                               int32_t window, hipStream_t st);
 
 }  // namespace vdx

@@ -2171,6 +2171,24 @@ __global__ void k_row_reset(RowState *__restrict__ rs, int32_t row0, int32_t row
   }
 }
 
+// State of rows [0, rows) for a call that brings its own history and uniforms
+// (no sampler object): each row's ring is the caller's `count[r]` ids (clamped
+// to [0, window]), its RNG words are zero (the uniforms are injected), and its
+// arrival ticket is cleared.  A kernel rather than a memset, so that a
+// captured call replays it.
+__global__ void k_rows_prepare(RowState *__restrict__ rs, uint32_t *__restrict__ tickets, int32_t rows,
+                               const int32_t *__restrict__ count, int32_t window) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  RowState s{};
+  const int32_t c = count ? count[r] : 0;
+  s.hist_count = window > 0 ? min(max(c, 0), window) : 0;
+  s.window = window;
+  s.ctr_row = r;
+  rs[r] = s;
+  tickets[r] = 0u;
+}
+
 // =============================================================================
 // Host launchers
 // =============================================================================
@@ -2238,6 +2256,13 @@ hipError_t launch_row_reset(RowState *rs, int32_t row0, int32_t rows, bool clear
   const int nb = (rows + 255) / 256;
   hipLaunchKernelGGL(k_row_reset, dim3(nb), dim3(256), 0, st, rs, row0, rows, clear_hist ? 1 : 0,
                      window, reseed ? 1 : 0, seed, add_row ? 1 : 0, pkey, prow);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_prepare(RowState *rs, uint32_t *tickets, int32_t rows, const int32_t *count,
+                               int32_t window, hipStream_t st) {
+  const int nb = (rows + 255) / 256;
+  hipLaunchKernelGGL(k_rows_prepare, dim3(nb), dim3(256), 0, st, rs, tickets, rows, count, window);
   return hipGetLastError();
 }
 

@@ -115,6 +115,9 @@ _SIGNATURES = {
     "vdx_sampler_process_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                              C.c_int64, C.c_void_p, C.POINTER(_Outputs),
                                              C.c_void_p]),
+    "vdx_sample_device_noalloc": (C.c_int, [C.POINTER(TVdxSamplerConfig), C.c_void_p, C.c_int32, C.c_int32,
+                                            C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                            C.POINTER(_Outputs), C.c_void_p]),
     "vdx_lmhead_q4_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                   C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
     "vdx_lmhead": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_float, C.c_int32,
@@ -495,6 +498,51 @@ def lmhead_pack(weights, wtype: int, in_dim: int, vocab: int, out=None, stream=N
 def lmhead_q4_0(weights, hidden, vocab: int, logits=None, scratch=None, stream=None):
     """The Q4_0 lm_head alone (matvec_q4_0.comp, batched), without the norm."""
     return lmhead(weights, VDX_TENSOR_Q4_0, hidden, vocab, logits=logits, scratch=scratch, stream=stream)
+
+
+def sample_device_noalloc(cfg: TVdxSamplerConfig, logits, uniforms, history=None, history_count=None,
+                          tokens=None, topk_idx=None, topk_prob=None, flags=None, uniforms_out=None,
+                          rows: int | None = None, vocab: int | None = None, row_stride: int | None = None,
+                          stream=None):
+    """vdx_sample_device_noalloc: samples device-resident rows with the
+    library's fixed workspace (no sampler object, nothing allocated by the
+    library).  ``uniforms`` (float32 GPU tensor, one per row) is required;
+    ``history`` (int32 GPU tensor, rows x stride) with ``history_count``
+    (int32 GPU tensor, one per row) gives each row's ring for the penalty.
+    Returns the int32 token tensor (``tokens`` when given)."""
+    import torch
+
+    assert logits.is_cuda and logits.dtype == torch.float32
+    if logits.dim() == 1:
+        logits = logits.view(1, -1)
+    B = int(logits.shape[0] if rows is None else rows)
+    V = int(logits.shape[-1] if vocab is None else vocab)
+    stride = int(logits.stride(0) if row_stride is None else row_stride)
+    assert uniforms.is_cuda and uniforms.dtype == torch.float32 and uniforms.numel() >= B
+    if tokens is None:
+        tokens = torch.empty(B, dtype=torch.int32, device=logits.device)
+    o = _Outputs()
+    o.tokens = tokens.data_ptr()
+    o.topk_idx = topk_idx.data_ptr() if topk_idx is not None else None
+    o.topk_prob = topk_prob.data_ptr() if topk_prob is not None else None
+    o.topk_stride = int(topk_idx.shape[-1] if topk_idx is not None else
+                        (topk_prob.shape[-1] if topk_prob is not None else 0))
+    o.flags = flags.data_ptr() if flags is not None else None
+    o.uniforms = uniforms_out.data_ptr() if uniforms_out is not None else None
+    hs = 0
+    if history is not None:
+        assert history.is_cuda and history.dtype == torch.int32 and history.dim() == 2
+        assert history_count is not None and history_count.dtype == torch.int32
+        hs = int(history.stride(0))
+    st = stream if stream is not None else torch.cuda.current_stream(logits.device)
+    rc = load_library().vdx_sample_device_noalloc(
+        C.byref(cfg), C.c_void_p(logits.data_ptr()), B, V, stride, C.c_void_p(uniforms.data_ptr()),
+        C.c_void_p(history.data_ptr()) if history is not None else None, hs,
+        C.c_void_p(history_count.data_ptr()) if history is not None else None, C.byref(o),
+        C.c_void_p(st.cuda_stream))
+    if rc < 0:
+        raise VdxSamplerError(rc, _err(None))
+    return tokens
 
 
 def version() -> str:
