@@ -42,8 +42,9 @@ struct vdx_sampler {
   hipStream_t aux[2] = {nullptr, nullptr};
   hipEvent_t ev_fork = nullptr;
   hipEvent_t ev_join[2] = {nullptr, nullptr};
-  // workspace (sized for ws_chunks chunks per row)
+  // workspace (sized for ws_chunks chunks per row, ws_cap candidate slots per chunk)
   int32_t ws_chunks = 0;
+  int32_t ws_cap = 0;
   ChunkMeta *d_meta = nullptr;
   Cand *d_cand = nullptr;
   FullMeta *d_fmeta = nullptr;
@@ -196,10 +197,13 @@ static int upload_row_params(vdx_sampler *s) {
 }
 
 // EnsureWorkspace (Sampler.pas:250-263) for the device path: grows the
-// per-row chunk records when a larger vocabulary is first seen.
-static int ensure_workspace(vdx_sampler *s, int32_t vocab) {
-  const int32_t S = chunks_for(vocab);
-  if (S <= s->ws_chunks) return VDX_OK;
+// per-row chunk records when a larger vocabulary (or a TopK needing more
+// candidate slots per chunk) is first seen.
+static int ensure_workspace(vdx_sampler *s, int32_t vocab, int32_t cap = kCandCap) {
+  const int32_t S0 = chunks_for(vocab);
+  if (S0 <= s->ws_chunks && cap <= s->ws_cap) return VDX_OK;
+  const int32_t S = S0 > s->ws_chunks ? S0 : s->ws_chunks;
+  if (cap < s->ws_cap) cap = s->ws_cap;
   HIP_TRY(s, hipStreamSynchronize(s->stream));
   (void)hipFree(s->d_meta);
   (void)hipFree(s->d_cand);
@@ -212,11 +216,12 @@ static int ensure_workspace(vdx_sampler *s, int32_t vocab) {
   s->ws_chunks = 0;
   const size_t rc = (size_t)s->max_rows * S;
   HIP_TRY(s, hipMalloc(&s->d_meta, rc * sizeof(ChunkMeta)));
-  HIP_TRY(s, hipMalloc(&s->d_cand, rc * kCandCap * sizeof(Cand)));
+  HIP_TRY(s, hipMalloc(&s->d_cand, rc * (size_t)cap * sizeof(Cand)));
   HIP_TRY(s, hipMalloc(&s->d_fmeta, rc * sizeof(FullMeta)));
   HIP_TRY(s, hipMalloc(&s->d_gpart, rc * sizeof(uint64_t)));
   // every record is written by its chunk before the row's last workgroup reads it
   s->ws_chunks = S;
+  s->ws_cap = cap;
   return VDX_OK;
 }
 
@@ -501,12 +506,14 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   const bool topk = path_any[1];
   if ((out->topk_idx || out->topk_prob) && topk && out->topk_stride < kmax)
     return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= TopK");
-  if (topk && kmax > kKMax)
-    return fail(s, VDX_E_UNSUPPORTED, "process_device: TopK > 64 is not implemented on the GPU");
+  if (topk && kmax > kKBig)
+    return fail(s, VDX_E_UNSUPPORTED, "process_device: TopK > 1024 is not implemented on the GPU");
   if (chunks_for(vocab) > kMaxChunks)
     return fail(s, VDX_E_UNSUPPORTED, "process_device: vocab > 4194304 is not supported");
+  // TopK > 64 runs the large-K kernel, with more candidate slots per chunk
+  const int32_t cap = (topk && kmax > kKMax) ? big_cand_cap(kmax, chunks_for(vocab)) : kCandCap;
   HIP_TRY(s, hipSetDevice(s->device));
-  int rc = ensure_workspace(s, vocab);
+  int rc = ensure_workspace(s, vocab, cap);
   if (rc != VDX_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
 
@@ -537,6 +544,7 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.out.flags = out->flags;
   p.meta = s->d_meta;
   p.cand = s->d_cand;
+  p.cand_cap = cap;
   p.fmeta = s->d_fmeta;
   p.gpart = s->d_gpart;
   p.tickets = s->d_tickets;
@@ -638,6 +646,7 @@ int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int3
   p.out.flags = out->flags;
   p.meta = reinterpret_cast<ChunkMeta *>(ws + kNaMeta);
   p.cand = reinterpret_cast<Cand *>(ws + kNaCand);
+  p.cand_cap = kCandCap;
   p.fmeta = reinterpret_cast<FullMeta *>(ws + kNaFullMeta);
   p.gpart = reinterpret_cast<uint64_t *>(ws + kNaGpart);
   p.tickets = reinterpret_cast<uint32_t *>(ws + kNaTickets);

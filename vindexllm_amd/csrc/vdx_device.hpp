@@ -17,10 +17,9 @@ constexpr int kKMax = 64;                      // top-K held one slot per lane
 constexpr int kCandCap = 128;                  // candidates stored per chunk
 constexpr int kMaxChunks = 256;                // V <= 4 Mi logits
 constexpr int kMergeCap = 2048;                // merge-phase LDS candidates
-constexpr int kReplayTile0 = 2048;             // first replay tile (logits)
-constexpr int kReplayTile = 4096;              // later replay tiles (logits)
-constexpr int kReplayCap = 2048;               // replay candidates per batch
 constexpr int kPenMax = 256;                   // history ids handled inside the top-K kernel
+constexpr int kKBig = 1024;                    // largest K of the large-K top-K kernel
+constexpr int kBigCandCap = 1024;              // its largest candidate slots per chunk
 
 // ---- per-row state kept in HBM -------------------------------------------------
 struct RowState {
@@ -60,6 +59,38 @@ __host__ __device__ __forceinline__ bool row_fuses_penalty(const RowCfg &c, int 
   return c.penalty != 1.0f && c.window <= kPenMax;
 }
 
+// Per-chunk candidate quota of the top-K stream phase.  A chunk stores every
+// logit >= tau_c, where tau_c guarantees >= Kq stored logits.  The merge
+// proves afterwards that the stored set holds the row's top K (theta = K-th
+// largest stored value >= every tau_c) or re-reads the chunks for which that
+// fails, so Kq may be far below K: the row's top K holds about K/S logits of
+// each of its S chunks.
+__host__ __device__ __forceinline__ int chunk_quota(int K, int S) {
+  if (S <= 1) return K;
+  const int q = (3 * K + S - 1) / S + 4;
+  return q < 8 ? (K < 8 ? K : 8) : (q < K ? q : K);
+}
+// The large-K kernel's quota: the row's top K holds about K/S logits of a
+// chunk, with a spread of about sqrt(K/S); four of those plus 8 leave the
+// re-read of a chunk rare while keeping the keys the merge selects from
+// (about S times the quota) within its LDS.
+__host__ __device__ __forceinline__ int big_chunk_quota(int K, int S) {
+  if (S <= 1) return K;
+  const int m = (K + S - 1) / S;
+  int r = 1;
+  while (r * r < m) ++r;  // ceil(sqrt(m))
+  const int q = m + 4 * r + 8;
+  return q < K ? q : K;
+}
+// Candidate slots per chunk of the large-K kernel: about three times the
+// quota (the stream phase's threshold stores up to ~2-3x it), at least 256.
+__host__ __device__ __forceinline__ int big_cand_cap(int K, int S) {
+  const int q = big_chunk_quota(K, S);
+  int cap = 256;
+  while (cap < 3 * q && cap < kBigCandCap) cap <<= 1;
+  return cap;
+}
+
 // Top-K stream phase: one record per (row, chunk):
 //   w    = tau_key | flags << 32  (every logit with key >= tau_key is stored;
 //                                  flags bit 0: a NaN or +inf logit was seen)
@@ -74,8 +105,8 @@ struct ChunkMeta {
 // Chunks are read in the interleaved layout (position j*1024 + wave*256 + ...),
 // so a short chunk of <= 256 logits lives in wave 0 and one of <= 512 in waves
 // 0 and 1.
-__device__ __forceinline__ int wave_cap(int clen) {
-  return clen <= 256 ? kCandCap : (clen <= 512 ? kCandCap / 2 : kCandCap / kWaves);
+__device__ __forceinline__ int wave_cap(int clen, int cap = kCandCap) {
+  return clen <= 256 ? cap : (clen <= 512 ? cap / 2 : cap / kWaves);
 }
 
 // A stored candidate: ord_key(value) << 32 | ~index (larger = better, unique).
@@ -205,6 +236,7 @@ struct OpMinU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
 struct OpAddU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
 struct OpOrU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a | b; } };
 struct OpMaxU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
+struct OpMinU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a < b ? a : b; } };
 struct OpAddF64 {
   __device__ uint64_t operator()(uint64_t a, uint64_t b) const {
     return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) + __longlong_as_double((long long)b));
@@ -222,6 +254,9 @@ __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return readlane64(wave_scan<uint64_t>(v, 0ull, OpMaxU64()), 63);
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  return readlane64(wave_scan<uint64_t>(v, ~0ull, OpMinU64()), 63);
 }
 // Maximum ignoring NaN (fmaxf): the ordered keys of non-NaN values, NaN as
 // the lowest key; an all-NaN wave yields NaN.

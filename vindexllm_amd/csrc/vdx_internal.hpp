@@ -30,6 +30,7 @@ struct CallParams {
   // workspace
   ChunkMeta *meta;
   Cand *cand;
+  int32_t cand_cap;     // candidate slots per chunk: kCandCap, or more when some row has K > 64
   FullMeta *fmeta;
   uint64_t *gpart;
   uint32_t *tickets;

@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kBlock) void k_penalty(CallParams p0) {
 // set sends the row to the exact replay, as the reference's min-buffer keeps
 // the tied logits that arrived first in its own slot order.
 //
-// Finish: see topk_fast and topk_replay.
+// Finish: see topk_fast and topk_exact.
 // =============================================================================
 constexpr int kMergeSpec = 8;   // candidate slots loaded per thread per round
 constexpr int kMergeTop = 512;  // keys >= T handled by the bitonic merge
@@ -277,10 +277,9 @@ struct TopkSmem {
   int32_t token;
   uint32_t rowflags;
   int32_t replay;
-  uint32_t jw[kReplayTile / kBlock][kWaves];
-  uint32_t jwbase[kReplayTile / kBlock][kWaves];
-  uint32_t ntile;
-  uint32_t minkey;
+  uint32_t xw[kWaves];   // exact path: candidates per wave in the current group
+  uint32_t xmkey;        // exact path: key of the buffer's minimum
+  int32_t xfrozen;       // exact path: L[0] is NaN, nothing enters
   int32_t qnan;
   float wfmax[kWaves];
   double S;
@@ -295,10 +294,6 @@ struct TopkSmem {
   uint64_t pbits[kBlock];  // history positions among each thread's 64 logits
   union {
     uint64_t sk[kMergeCap];
-    struct {
-      float v[kReplayCap];
-      int32_t i[kReplayCap];
-    } rc;
   } buf;
 };
 
@@ -313,11 +308,7 @@ __device__ __forceinline__ float gmax4(const float (&v)[kPerThread], int j) {
 // set holds the row's top K (theta = K-th largest stored value >= every tau_c)
 // or re-reads the chunks for which that fails, so Kq may be far below K: the
 // row's top 64 holds about 64/S logits of each of its S chunks.
-__device__ __forceinline__ int chunk_quota(int K, int S) {
-  if (S <= 1) return K;
-  const int q = (3 * K + S - 1) / S + 4;
-  return min(K, max(8, q));
-}
+
 
 // Repetition penalty fused into the top-K kernel (Sampler.pas:285-303): each
 // workgroup penalises the history ids that fall in its own chunk, in its
@@ -519,11 +510,12 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p0) {
   }
 }
 
-template <bool VEC>
+// `ccap`: candidate slots of a full chunk (kCandCap, or more for large K).
+template <bool VEC, class SM>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
                                             ChunkMeta *__restrict__ meta, const PenaltyPrefetch &pf,
-                                            TopkSmem &sm) {
+                                            SM &sm, int ccap = kCandCap) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
   float v[kPerThread];
@@ -565,7 +557,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   uint32_t tau = 0u;
   if (fastthr) {
     tau = min(min(sm.wmax[0], sm.wmax[1]), min(sm.wmax[2], sm.wmax[3]));
-  } else if (clen > kCandCap) {
+  } else if (clen > ccap) {
     // the largest of 64 sampled thread maxima (wave 0's) that >= Kq reach
     uint32_t mycnt = 0u;
 #pragma unroll 4
@@ -588,7 +580,7 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   // group maximum per compare and branch (wave-uniform) only into groups in
   // which some lane passes.
   const bool all = (tau == 0u);
-  const int cap = wave_cap(clen);
+  const int cap = wave_cap(clen, ccap);
   Cand *wreg = cand + wv * cap;
   uint32_t wc = 0u;  // wave-uniform
   if (clen == kChunk && !all) {
@@ -645,8 +637,8 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
 // logits share it and sm.rneed of them are in the top K.
 // Bytes above the highest byte in which kmin and kmax (bounds of the keys)
 // differ are common to every key and are not scanned.
-__device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, TopkSmem &sm, uint32_t kmin,
-                                              uint32_t kmax) {
+template <class SM>
+__device__ __forceinline__ uint32_t radix_kth(uint32_t n, int K, SM &sm, uint32_t kmin, uint32_t kmax) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t d = kmin ^ kmax;
   if (d == 0u) {  // every key shares one value
@@ -1444,126 +1436,236 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
   }
 }
 
-// Exact replay of the reference min-buffer (Sampler.pas:341-383) and the
-// slot-order finish (:385-459).  Whole workgroup.
-__device__ __forceinline__ void topk_replay(const CallParams &p, int row, TopkSmem &sm) {
+// ---- Exact path: the reference's min-buffer (Sampler.pas:341-383) replayed over
+// the logits that can enter it, then the slot-order finish (:385-459).
+//
+// The buffer (K <= 64) lives in wave 0, one entry per lane, sorted ascending:
+//   entry = slot_key(value) << 32 | slot << 22 | index
+// so lane 0 holds the reference's "first strict minimum" (smallest value,
+// then lowest slot; NaN sorts above +inf and is never the minimum).  A logit
+// x enters iff x > that minimum: it takes the minimum's slot, the minimum
+// leaves (lane 0), and x is inserted at its rank among the rest (lanes
+// shift down by one), i.e. one 64-bit compare, a ballot and a DPP lane shift.
+//
+// Only logits above the current minimum can enter, and the minimum only
+// rises, so the chunks are walked in index order: a chunk whose stored
+// candidates include every logit above the current minimum (its threshold
+// tau_c is at most one key above it and no region overflowed) feeds those,
+// sorted by index; any other chunk (always chunk 0) is re-read and fed one
+// 1024-logit group at a time, each group filtered against the minimum left
+// by the previous one.
+__device__ __forceinline__ uint64_t wave_shl1_64(uint64_t v) {  // lane l <- lane l + 1
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+constexpr uint32_t kXbIdxMask = (1u << 22) - 1u;
+static_assert(kMaxChunks * kChunk <= (1 << 22) && kKMax <= 64, "buffer entry packing");
+
+struct MinBuf {
+  uint64_t b;      // lane l < K: the l-th smallest entry; lanes >= K: ~0
+  uint32_t mkey;   // slot_key of the minimum (lane 0)
+  uint32_t mslot;  // its slot
+};
+__device__ __forceinline__ void mb_refresh(MinBuf &m) {
+  const uint64_t b0 = readlane64(m.b, 0);
+  m.mkey = (uint32_t)(b0 >> 32);
+  m.mslot = ((uint32_t)b0 >> 22) & 63u;
+}
+// Logit (key xk, index xi) enters: it replaces the minimum in the minimum's slot.
+__device__ __forceinline__ void mb_enter(MinBuf &m, uint32_t xk, uint32_t xi) {
+  const uint64_t nk = ((uint64_t)xk << 32) | ((uint64_t)m.mslot << 22) | xi;
+  const int pp = __popcll(__ballot(m.b < nk) & ~1ull);  // its rank once lane 0 has left
+  const uint64_t sh = wave_shl1_64(m.b);
+  const int lane = lane_id();
+  m.b = (lane < pp) ? sh : ((lane == pp) ? nk : m.b);
+  mb_refresh(m);
+}
+// One logit per lane, lane order = index order; `has` marks real entries.
+// Keys are ord_key of non-NaN logits (NaN never enters: Sampler.pas:369).
+__device__ __forceinline__ void mb_feed(MinBuf &m, bool has, uint32_t ck, uint32_t ci) {
+  uint64_t pend = __ballot(has && ck > m.mkey);
+  while (pend) {
+    const int src = __ffsll((unsigned long long)pend) - 1;
+    mb_enter(m, readlane32(ck, src), readlane32(ci, src));
+    pend &= ~(1ull << src);
+    pend &= __ballot(ck > m.mkey);
+  }
+}
+
+// Re-reads chunk [c0, c0 + clen) of L into v (interleaved layout); rows the
+// fused penalty wrote in place are read past the caches.
+template <bool VEC>
+__device__ __forceinline__ void reload_chunk(const float *L, int c0, int clen, bool penalised,
+                                             float (&v)[kPerThread]) {
+  const int lane = lane_id(), wv = threadIdx.x >> 6;
+  if (VEC) {
+#pragma unroll
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      const int local = chunk_pos(wv, lane, 4 * j);
+      const float *q = L + c0 + (local < clen ? local : 0);
+      const f32x4 f = penalised ? xload4(q) : __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q));
+      v[4 * j + 0] = f[0];
+      v[4 * j + 1] = f[1];
+      v[4 * j + 2] = f[2];
+      v[4 * j + 3] = f[3];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int local = chunk_pos(wv, lane, i);
+      const float *q = L + c0 + (local < clen ? local : 0);
+      v[i] = penalised ? xloadf(q) : *q;
+    }
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_exact(const CallParams &p, int row, const ChunkMeta *__restrict__ cm,
+                                           const Cand *__restrict__ cand_row, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int K = p.top_k, V = p.vocab;
+  const int K = p.top_k, V = p.vocab, S = p.nchunks;
   const float *L = p.logits + (int64_t)row * p.stride;
-  constexpr int kJ = kReplayTile / kBlock;
+  const bool pen = p.fuse_penalty != 0;
 
-  // fill: slots 0..K-1 hold logits 0..K-1 (wave 0, one slot per lane)
-  float sv = 0.0f;
-  int32_t si = -1;
-  uint32_t skey = 0xFFFFFFFFu, mkey = 0xFFFFFFFFu;
-  int mi = 0;
-  float tmax = -INFINITY;
-  const float l0v = xloadf(&L[0]);
-  const bool frozen = (l0v != l0v);  // NaN in slot 0: nothing ever enters
+  // chunk records: stored counts and thresholds (an overflowed chunk is "open")
+  for (int c = tid; c < S; c += kBlock) {
+    const uint64_t w0 = xload(&cm[c].w);
+    const uint64_t n01 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[0]));
+    const uint64_t n23 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[2]));
+    const uint32_t cap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk));
+    const uint32_t n0 = (uint32_t)n01, n1 = (uint32_t)(n01 >> 32), n2 = (uint32_t)n23,
+                   n3 = (uint32_t)(n23 >> 32);
+    const bool ovf = n0 > cap || n1 > cap || n2 > cap || n3 > cap;
+    sm.ccount[c] = min(n0, cap) | (min(n1, cap) << 8) | (min(n2, cap) << 16) | (min(n3, cap) << 24);
+    sm.ctau[c] = ovf ? 0xFFFFFFFFu : (uint32_t)w0;
+  }
+  MinBuf mb{~0ull, 0xFFFFFFFFu, 0u};
+  uint64_t *list = sm.buf.sk;  // one group's candidates in index order: ord_key << 32 | index
+  float v[kPerThread];
+  for (int c = 0; c < S; ++c) {
+    const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+    __syncthreads();  // sm.ctau / the previous chunk's list and sm.xmkey
+    const uint32_t mk = (c == 0) ? 0u : sm.xmkey;
+    if (c > 0 && (sm.xfrozen || mk == 0xFFFFFFFFu)) break;  // nothing can enter any more
+    const uint32_t tc = sm.ctau[c];
+    if (c > 0 && tc <= mk + 1u) {
+      // every logit above the minimum was stored: wave 0 feeds them by index
+      if (wv == 0) {
+        const Cand *cc = cand_row + (int64_t)c * kCandCap;
+        const uint32_t cap = (uint32_t)wave_cap(clen);
+        const int sh = cap == 128u ? 7 : (cap == 64u ? 6 : 5);
+        const uint32_t cnt = sm.ccount[c];
+        uint64_t x[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const uint32_t slot = 2u * (uint32_t)lane + (uint32_t)e;
+          const uint64_t k = xload(&cc[slot]);
+          const bool ok = (slot & (cap - 1u)) < ((cnt >> (8 * (slot >> sh))) & 0xFFu) &&
+                          (uint32_t)(k >> 32) > mk;
+          // sorted by index: index << 32 | key
+          x[e] = ok ? (((uint64_t)(~(uint32_t)k) << 32) | (k >> 32)) : ~0ull;
+        }
+        if (__ballot(x[0] != ~0ull || x[1] != ~0ull)) {
+          wave_sort2(x[1], x[0]);  // x[1] descending, x[0] ascending
+          const uint64_t lo = x[0] < x[1] ? x[0] : x[1], hi = x[0] < x[1] ? x[1] : x[0];
+          x[0] = wave_merge<true>(lo);
+          x[1] = wave_merge<true>(hi);
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            mb_feed(mb, x[e] != ~0ull, (uint32_t)x[e], (uint32_t)(x[e] >> 32));
+        }
+        if (lane == 0) sm.xmkey = mb.mkey;
+      }
+      continue;
+    }
+    // re-read the chunk and feed it one 1024-logit group at a time
+    reload_chunk<VEC>(L, c0, clen, pen, v);
+    if (c == 0) {
+      // the first K logits fill slots 0..K-1 (Sampler.pas:352-366); a NaN at
+      // index 0 stays the minimum and nothing ever enters (:369)
+      if (wv == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (lane * 4 + e < kKMax) sm.q[lane * 4 + e] = v[e];
+      }
+      __syncthreads();
+      if (wv == 0) {
+        const float x = sm.q[lane];
+        mb.b = (lane < K) ? (((uint64_t)slot_key(x) << 32) | ((uint64_t)lane << 22) | (uint32_t)lane) : ~0ull;
+        mb.b = wave_sort<true>(mb.b);
+        mb_refresh(mb);
+        const float l0 = sm.q[0];
+        if (lane == 0) {
+          sm.xfrozen = (l0 != l0) ? 1 : 0;
+          sm.xmkey = mb.mkey;
+        }
+      }
+    }
+    // unrolled: a register array indexed by a loop variable would live in scratch
+#pragma unroll
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      __syncthreads();  // sm.xmkey of the previous group; the list is free
+      if (sm.xfrozen) break;
+      const uint32_t m = sm.xmkey;
+      if (m == 0xFFFFFFFFu) break;  // uniform
+      const int base = j * 1024 + wv * 256 + lane * 4;
+      float g4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g4[e] = v[4 * j + e];
+      uint32_t bits = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = g4[e];
+        const int loc = base + e;
+        const bool ok = loc < clen && (c0 + loc) >= K && x == x && ord_key(x) > m;
+        bits |= ok ? (1u << e) : 0u;
+      }
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wave_incl_scan_u32(cnt);
+      if (lane == 63) sm.xw[wv] = incl;
+      __syncthreads();
+      uint32_t off = incl - cnt, total = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        off += (w < wv) ? sm.xw[w] : 0u;
+        total += sm.xw[w];
+      }
+      if (total == 0u) continue;  // uniform
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if ((bits >> e) & 1u) {
+          list[off++] = ((uint64_t)ord_key(g4[e]) << 32) | (uint32_t)(c0 + base + e);
+        }
+      }
+      __syncthreads();
+      if (wv == 0) {
+        for (uint32_t g = 0u; g < total; g += 64u) {
+          const bool has = g + (uint32_t)lane < total;
+          const uint64_t en = has ? list[g + lane] : 0ull;
+          mb_feed(mb, has, (uint32_t)(en >> 32), (uint32_t)en);
+        }
+        if (lane == 0) sm.xmkey = mb.mkey;
+      }
+    }
+  }
+  __syncthreads();
+  // slot order; the running maximum M (strict '>' from L[0]): NaN when L[0]
+  // is NaN, else the largest non-NaN logit, which is in the buffer
+  const bool frozen = sm.xfrozen != 0;
   if (wv == 0) {
+    const uint32_t key = (uint32_t)(mb.b >> 32);
+    const float x = (key == 0xFFFFFFFFu) ? __builtin_nanf("") : key_float(key);
     if (lane < K) {
-      sv = xloadf(&L[lane]);
-      si = lane;
-      skey = slot_key(sv);
-      tmax = fmaxf(tmax, sv);
+      const int s = (int)(((uint32_t)mb.b >> 22) & 63u);
+      sm.slot_v[s] = x;
+      sm.slot_i[s] = (int32_t)((uint32_t)mb.b & kXbIdxMask);
     }
-    if (!frozen) {
-      mkey = wave_min_u32(lane < K ? skey : 0xFFFFFFFFu);
-      mi = __ffsll((unsigned long long)__ballot(lane < K && skey == mkey)) - 1;
-    }
-    if (lane == 0) sm.minkey = mkey;
+    const float wm = wave_max_f32(lane < K ? x : __builtin_nanf(""));
+    if (lane == 0) sm.wfmax[0] = wm;
   }
   __syncthreads();
-
-  if (!frozen) {
-    int t0 = K;
-    int tend = min(V, kReplayTile0);
-    while (t0 < V) {
-      const int tl = tend - t0;
-      const uint32_t thr = sm.minkey;
-      float v[kJ];
-      uint32_t pm = 0u;
-#pragma unroll
-      for (int j = 0; j < kJ; ++j) {
-        const int e = j * kBlock + tid;
-        v[j] = (e < tl) ? xloadf(&L[t0 + e]) : __builtin_nanf("");
-      }
-#pragma unroll
-      for (int j = 0; j < kJ; ++j) {
-        tmax = fmaxf(tmax, v[j]);
-        const bool pass = (v[j] == v[j]) && (ord_key(v[j]) > thr);
-        pm |= pass ? (1u << j) : 0u;
-        const uint64_t b = __ballot(pass);
-        if (lane == 0) sm.jw[j][wv] = (uint32_t)__popcll(b);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t acc = 0u;
-        for (int j = 0; j < kJ; ++j)
-          for (int w = 0; w < kWaves; ++w) {
-            sm.jwbase[j][w] = acc;
-            acc += sm.jw[j][w];
-          }
-        sm.ntile = acc;
-      }
-      __syncthreads();
-      const uint32_t nt = sm.ntile;
-      for (uint32_t b0 = 0u; b0 < nt; b0 += (uint32_t)kReplayCap) {
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          const bool pj = (pm >> j) & 1u;
-          const uint64_t b = __ballot(pj);
-          if (pj) {
-            const uint32_t pos = sm.jwbase[j][wv] + (uint32_t)__popcll(b & lanemask_lt());
-            if (pos >= b0 && pos < b0 + (uint32_t)kReplayCap) {
-              sm.buf.rc.v[pos - b0] = v[j];
-              sm.buf.rc.i[pos - b0] = t0 + j * kBlock + tid;
-            }
-          }
-        }
-        __syncthreads();
-        if (wv == 0) {
-          const uint32_t nb = min(nt - b0, (uint32_t)kReplayCap);
-          for (uint32_t g = 0u; g < nb; g += 64u) {
-            const bool has = g + (uint32_t)lane < nb;
-            const float cv = has ? sm.buf.rc.v[g + lane] : 0.0f;
-            const int32_t ci = has ? sm.buf.rc.i[g + lane] : 0;
-            const uint32_t ck = has ? ord_key(cv) : 0u;
-            uint64_t pend = __ballot(has && ck > mkey);
-            while (pend) {
-              const int src = __ffsll((unsigned long long)pend) - 1;
-              const uint32_t ek = readlane32(ck, src);
-              const float ev = __uint_as_float(readlane32(__float_as_uint(cv), src));
-              const int32_t ei = (int32_t)readlane32((uint32_t)ci, src);
-              if (lane == mi) {
-                skey = ek;
-                sv = ev;
-                si = ei;
-              }
-              mkey = wave_min_u32(lane < K ? skey : 0xFFFFFFFFu);
-              mi = __ffsll((unsigned long long)__ballot(lane < K && skey == mkey)) - 1;
-              pend &= ~(1ull << src);
-              pend &= __ballot(ck > mkey);
-            }
-          }
-          if (lane == 0) sm.minkey = mkey;
-        }
-        __syncthreads();
-      }
-      t0 = tend;
-      tend = min(V, t0 + kReplayTile);
-    }
-  }
-  // running maximum M (strict '>' from L[0]: NaN at 0 sticks, later NaN skipped)
-  const float wm = wave_max_f32(tmax);
-  if (lane == 0) sm.wfmax[wv] = wm;
-  if (wv == 0 && lane < K) {
-    sm.slot_v[lane] = sv;
-    sm.slot_i[lane] = si;
-  }
-  __syncthreads();
-  const float M = frozen ? __builtin_nanf("")
-                         : fmaxf(fmaxf(sm.wfmax[0], sm.wfmax[1]), fmaxf(sm.wfmax[2], sm.wfmax[3]));
+  const float M = frozen ? __builtin_nanf("") : sm.wfmax[0];
 
   // softmax over the slots (:385-391)
   if (wv == 0) {
@@ -1727,12 +1829,745 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
   }
   if (mr < 0) mr = topk_merge<VEC>(p, L, S, cm, cr, sm) ? 1 : 0;
   if (mr > 0) topk_fast(p, row, sm);
-  if (sm.replay) topk_replay(p, row, sm);
+  if (sm.replay) topk_exact<VEC>(p, row, cm, cr, sm);
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
   }
 }
+
+// =============================================================================
+// Top-K for 64 < K <= kKBig (Sampler.pas:327-460).
+//
+// The stream phase is the one above with more candidate slots per chunk
+// (ccap, sized from the chunk quota).  The merge (the row's last workgroup)
+// gathers the stored keys into LDS -- only those >= T = max_c tau_c when no
+// chunk overflowed, since every logit >= T was stored -- selects theta = the
+// K-th largest by radix, re-reads any chunk whose unstored logits could reach
+// theta, and sorts the K keys >= theta across the workgroup.  The finish runs
+// over them, four per thread; rows it cannot settle exactly take the exact
+// path, whose buffer is a two-level tournament in LDS.
+// =============================================================================
+constexpr int kBigCap = 4096;  // merge-phase LDS keys
+static_assert(kKBig <= 1024 && kKBig % kBlock == 0, "large-K layout: 4 sorted keys per thread");
+
+struct TopkBigSmem {
+  // stream phase (the fields topk_stream and the fused penalty use)
+  uint32_t thr[64];
+  uint32_t cnt[kWaves][64];
+  uint32_t wmax[kWaves];
+  uint32_t wflag[kWaves];
+  int32_t last;
+  uint32_t ptab[kPenHash];
+  uint64_t pbits[kBlock];
+  // merge
+  uint32_t ctau[kMaxChunks];
+  uint64_t ccnt[kMaxChunks];  // stored keys per wave region, 16 bits each
+  uint32_t hist[256];
+  uint32_t rbin, rneed, rcnt;
+  uint32_t n;
+  int32_t ntop;
+  int32_t flag;
+  // finish
+  float uval;
+  int32_t token;
+  uint32_t rowflags;
+  int32_t replay;
+  float qmax;
+  int32_t pos;
+  int32_t amb;
+  double wtot[kWaves];
+  double S;
+  // exact path
+  uint32_t xw[kWaves];
+  uint32_t xmkey;
+  int32_t xfrozen;
+  int32_t qnan;
+  float wfmax[kWaves];
+  uint64_t topkey[kKBig];  // the top K, descending (value, then lower index)
+  union {
+    uint64_t sk[kBigCap];
+    struct {
+      uint64_t list[1024];   // one group's candidates / sort keys
+      uint64_t leaf[kKBig];  // buffer slot s: slot_key << 32 | index
+      float q[kKBig];
+      float q_ord[kKBig];
+      int32_t i_ord[kKBig];
+      float v_ord[kKBig];
+    } x;
+  } buf;
+};
+
+// Stored keys of region r (0..3) of a chunk record.
+__device__ __forceinline__ uint32_t big_count(uint64_t ccnt, int r) { return (uint32_t)(ccnt >> (16 * r)) & 0xFFFFu; }
+
+// Descending bitonic sort of a[0, N) in LDS (N a power of two, whole workgroup).
+__device__ __forceinline__ void block_sort_desc(uint64_t *a, int N) {
+  for (int k2 = 2; k2 <= N; k2 <<= 1) {
+    for (int j = k2 >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < N; i += kBlock) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = a[i], y = a[ixj];
+          const bool desc = (i & k2) == 0;
+          if ((x < y) == desc) {
+            a[i] = y;
+            a[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Appends the stored keys >= lo of every chunk (all slots of each wave region
+// below its count) to sm.buf.sk and returns how many there were (more than
+// kBigCap: not all were kept).  Thread t takes a contiguous run of the
+// concatenated regions; it locates each item (binary search over the
+// per-chunk offsets, then the chunk's four regions) before issuing its loads,
+// so they are in flight together.
+__device__ __forceinline__ uint32_t big_gather(const Cand *__restrict__ cand_row, int S, int V, int ccap,
+                                               uint32_t lo, TopkBigSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t *off = sm.hist;  // per-chunk start in the concatenation (S <= 256)
+  uint32_t tot = 0u;
+  if (tid < S) {
+    const uint64_t cc = sm.ccnt[tid];
+    tot = big_count(cc, 0) + big_count(cc, 1) + big_count(cc, 2) + big_count(cc, 3);
+  }
+  const uint32_t incl = wave_incl_scan_u32(tot);
+  if (lane == 63) sm.xw[wv] = incl;
+  if (tid == 0) sm.n = 0u;
+  __syncthreads();
+  uint32_t base = 0u, all = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    base += (w < wv) ? sm.xw[w] : 0u;
+    all += sm.xw[w];
+  }
+  if (tid < S) off[tid] = base + incl - tot;
+  __syncthreads();
+  const uint32_t per = (all + kBlock - 1) / kBlock;
+  for (uint32_t g0 = 0u; g0 < per; g0 += 16u) {
+    uint64_t kk[16];
+    const Cand *addr[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t g = (uint32_t)tid * per + g0 + (uint32_t)i;
+      addr[i] = nullptr;
+      if (g0 + (uint32_t)i < per && g < all) {
+        int a = 0, b = S - 1;  // the last chunk whose offset is <= g
+        while (a < b) {
+          const int mid = (a + b + 1) >> 1;
+          if (off[mid] <= g) a = mid; else b = mid - 1;
+        }
+        const uint64_t cc = sm.ccnt[a];
+        uint32_t rel = g - off[a];
+        int r = 0;
+        while (r < kWaves - 1 && rel >= big_count(cc, r)) rel -= big_count(cc, r++);
+        const uint32_t rcap = (uint32_t)wave_cap(min(kChunk, V - a * kChunk), ccap);
+        addr[i] = cand_row + (int64_t)a * ccap + (int64_t)r * rcap + rel;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kk[i] = addr[i] ? xload(addr[i]) : 0ull;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (addr[i] && (uint32_t)(kk[i] >> 32) >= lo) {
+        const uint32_t q = atomicAdd(&sm.n, 1u);
+        if (q < (uint32_t)kBigCap) sm.buf.sk[q] = kk[i];
+      }
+    }
+  }
+  __syncthreads();
+  return sm.n;
+}
+
+// Block-wide OR / max of one value per thread (through sm.xw).
+__device__ __forceinline__ uint32_t block_or_u32(uint32_t v, TopkBigSmem &sm) {
+  v = wave_or_u32(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sm.xw[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return sm.xw[0] | sm.xw[1] | sm.xw[2] | sm.xw[3];
+}
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, TopkBigSmem &sm) {
+  v = wave_max_u32(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sm.xw[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(sm.xw[0], sm.xw[1]), max(sm.xw[2], sm.xw[3]));
+}
+
+// Merge for large K.  Returns true when sm.topkey[0, K) holds the row's top K
+// (descending value, then lower index); false when the exact path must run:
+// a NaN or +inf logit, the K-th value tied with a logit outside the set (the
+// reference's slot order decides which tied logits it keeps), or more keys
+// than the merge's LDS holds.
+template <bool VEC>
+__device__ __forceinline__ bool topk_merge_big(const CallParams &p, const float *__restrict__ L, int S,
+                                               const ChunkMeta *__restrict__ cm, const Cand *__restrict__ cand_row,
+                                               int ccap, TopkBigSmem &sm) {
+  const int V = p.vocab, K = p.top_k;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t fl = 0u, tmx = 0u;
+  for (int c = tid; c < S; c += kBlock) {
+    const uint64_t w0 = xload(&cm[c].w);
+    const uint64_t n01 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[0]));
+    const uint64_t n23 = xload(reinterpret_cast<const uint64_t *>(&cm[c].n[2]));
+    const uint32_t rcap = (uint32_t)wave_cap(min(kChunk, V - c * kChunk), ccap);
+    const uint32_t n0 = (uint32_t)n01, n1 = (uint32_t)(n01 >> 32), n2 = (uint32_t)n23,
+                   n3 = (uint32_t)(n23 >> 32);
+    const bool ovf = n0 > rcap || n1 > rcap || n2 > rcap || n3 > rcap;
+    sm.ccnt[c] = (uint64_t)min(n0, rcap) | ((uint64_t)min(n1, rcap) << 16) | ((uint64_t)min(n2, rcap) << 32) |
+                 ((uint64_t)min(n3, rcap) << 48);
+    const uint32_t tau = ovf ? 0xFFFFFFFFu : (uint32_t)w0;
+    sm.ctau[c] = tau;
+    tmx = max(tmx, tau);
+    fl |= (uint32_t)(w0 >> 32);
+  }
+  fl = block_or_u32(fl, sm);
+  tmx = block_max_u32(tmx, sm);
+  if (fl) return false;
+  // Every logit >= T = max tau_c was stored when no chunk overflowed, so if
+  // at least K stored keys reach T the top K is among them.
+  uint32_t n = 0u, theta = 0u;
+  bool done = false;
+  if (tmx != 0xFFFFFFFFu) {
+    n = big_gather(cand_row, S, V, ccap, tmx, sm);
+    if (n >= (uint32_t)K && n <= (uint32_t)kBigCap) {
+      theta = radix_kth(n, K, sm, tmx, 0xFFFFFFFFu);
+      done = true;
+    }
+  }
+  if (!done) {
+    // every stored key; theta = the K-th largest (a lower bound of the row's
+    // K-th value); chunks whose unstored logits could reach it are re-read
+    n = big_gather(cand_row, S, V, ccap, 0u, sm);
+    if (n > (uint32_t)kBigCap) return false;
+    theta = (n >= (uint32_t)K) ? radix_kth(n, K, sm, 0u, 0xFFFFFFFFu) : 0u;
+    for (int round = 0; round < 2; ++round) {
+      int open = 0;
+      for (int c = tid; c < S; c += kBlock) open |= (sm.ctau[c] > theta) ? 1 : 0;
+      open = __syncthreads_or(open);
+      if (!open) break;
+      if (round == 1) return false;  // re-read chunks are closed: not reached
+      // keep the stored keys >= theta of closed chunks, then append every
+      // logit >= theta of the open ones
+      uint64_t keep[kBigCap / kBlock];
+#pragma unroll
+      for (int r = 0; r < kBigCap / kBlock; ++r) {
+        const uint32_t i = (uint32_t)(tid + r * kBlock);
+        keep[r] = 0ull;
+        if (i < n) {
+          const uint64_t k = sm.buf.sk[i];
+          const int c = (int)((~(uint32_t)k) / (uint32_t)kChunk);
+          if ((uint32_t)(k >> 32) >= theta && sm.ctau[c] <= theta) keep[r] = k;
+        }
+      }
+      __syncthreads();
+      if (tid == 0) sm.n = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < kBigCap / kBlock; ++r) {
+        if (keep[r]) {
+          const uint32_t q = atomicAdd(&sm.n, 1u);
+          sm.buf.sk[q] = keep[r];
+        }
+      }
+      for (int c = 0; c < S; ++c) {
+        if (sm.ctau[c] <= theta) continue;  // uniform
+        const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+        float v[kPerThread];
+        reload_chunk<VEC>(L, c0, clen, p.fuse_penalty != 0, v);
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+          const int local = chunk_pos(wv, lane, i);
+          const float x = v[i];
+          if (local < clen && x == x && ord_key(x) >= theta) {
+            const uint32_t q = atomicAdd(&sm.n, 1u);
+            if (q < (uint32_t)kBigCap) sm.buf.sk[q] = ((uint64_t)ord_key(x) << 32) | (uint32_t)(~(uint32_t)(c0 + local));
+          }
+        }
+      }
+      __syncthreads();
+      for (int c = tid; c < S; c += kBlock)
+        if (sm.ctau[c] > theta) sm.ctau[c] = theta;  // now closed
+      n = sm.n;
+      if (n > (uint32_t)kBigCap || n < (uint32_t)K) return false;
+      theta = radix_kth(n, K, sm, 0u, 0xFFFFFFFFu);
+    }
+    if (n < (uint32_t)K) return false;
+  }
+  if (sm.rcnt > sm.rneed) return false;  // the K-th value is tied outside the set
+  // the K keys >= theta, sorted descending (padded to a power of two with 0)
+  int N = 1;
+  while (N < K) N <<= 1;
+  for (int i = tid; i < N; i += kBlock) sm.topkey[i] = 0ull;
+  __syncthreads();
+  if (tid == 0) sm.n = 0u;
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += kBlock) {
+    const uint64_t k = sm.buf.sk[i];
+    if ((uint32_t)(k >> 32) >= theta) {
+      const uint32_t q = atomicAdd(&sm.n, 1u);
+      if (q < (uint32_t)kKBig) sm.topkey[q] = k;
+    }
+  }
+  __syncthreads();
+  block_sort_desc(sm.topkey, N);
+  return true;
+}
+
+// Block-wide exclusive scan of one double per thread; returns the prefix and
+// sets `total` (every thread).
+__device__ __forceinline__ double big_excl_scan(double x, double &total, TopkBigSmem &sm) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const double incl = wave_incl_scan_f64(x);
+  __syncthreads();
+  if (lane == 63) sm.wtot[wv] = incl;
+  __syncthreads();
+  double base = 0.0;
+  total = 0.0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wv) base += sm.wtot[w];
+    total += sm.wtot[w];
+  }
+  return base + (incl - x);
+}
+
+// Finish over the sorted top K (Sampler.pas:385-459), thread t holding
+// entries 4t..4t+3.  q = fl32(exp((v - M) invT)) as the reference computes
+// it; Min-P, the Top-P cut and the draw follow :393-459 in value order,
+// which is the reference's sorted order except inside groups of equal q.
+// Sums are block scans.  When every non-zero q is within 2^f of the largest
+// (f = 29 - ceil(log2 K)), each q is a multiple of 2^(e-f-23) (e the
+// exponent of q_max) and any sum of K of them has at most 53 bits, so every
+// partial sum is exact in any order and equals the reference's.  Otherwise
+// each sum of K non-negative terms is within 2 K 2^-53 of the exact one in
+// any order, so a comparison of a running sum with the Top-P target or the
+// draw threshold that falls within the combined bound could go either way
+// in the reference's order: such rows, a Top-P cut or a draw inside a group
+// of equal q, Top-P >= 1 (the draw walks the reference's slot order), and the
+// fallback (no running sum exceeds the threshold) take the exact path.
+__device__ __forceinline__ void topk_finish_big(const CallParams &p, int row, TopkBigSmem &sm) {
+  const int tid = threadIdx.x;
+  const int K = p.top_k;
+  const float M = key_float((uint32_t)(sm.topkey[0] >> 32));
+  bool elig = (p.top_p < 1.0f) && (p.inv_t > 0.0f) && (p.inv_t <= 3.4028235e38f);
+  float q[4];
+  int32_t id[4];
+  bool act[4];
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = 4 * tid + i;
+    act[i] = k < K;
+    const uint64_t key = act[i] ? sm.topkey[k] : 0ull;
+    id[i] = (int32_t)(~(uint32_t)key);
+    q[i] = act[i] ? (float)exp(((double)key_float((uint32_t)(key >> 32)) - (double)M) * (double)p.inv_t) : 0.0f;
+    bad = bad || (act[i] && !(q[i] <= 3.4028235e38f));
+  }
+  if (tid == 0) sm.qmax = q[0];
+  __syncthreads();
+  const float qmax = sm.qmax;
+  int lk = 0;
+  while ((1 << lk) < K) ++lk;
+  const float qfloor = ldexpf(qmax, -(29 - lk));
+  bool inexact = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) inexact = inexact || (act[i] && q[i] != 0.0f && q[i] < qfloor);
+  const uint32_t badm = block_or_u32((bad ? 1u : 0u) | (inexact ? 2u : 0u), sm);
+  elig = elig && !(badm & 1u);
+  const bool exact = !(badm & 2u);
+  if (elig && p.min_p > 0.0f) {  // Min-P (:393-410): Qmax = q[0]
+    const float thr = qmax * p.min_p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = (q[i] < thr) ? 0.0f : q[i];
+  }
+  // running sums in value order
+  double loc[4], s = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    loc[i] = s;
+    s = s + (double)q[i];
+  }
+  double S1;
+  const double base = big_excl_scan(s, S1, sm);
+  const double target = (double)p.top_p * S1;
+  const double Kd = (double)K;
+  const double err1 = exact ? 0.0 : (4.0 * Kd * 0x1p-53 * S1 * (1.0 + (double)p.top_p) + 0x1p-50 * target);
+  bool kept[4], near = false;
+  double s2 = 0.0;
+  float qk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const double C = base + loc[i];
+    kept[i] = act[i] && q[i] > 0.0f && C < target;  // Top-P (:431-444)
+    near = near || (act[i] && q[i] > 0.0f && err1 > 0.0 && fabs(C - target) <= err1);
+    qk[i] = kept[i] ? q[i] : 0.0f;
+  }
+  // the cut must not split a group of equal q (the reference keeps the members
+  // that come first in its slot order): the first dropped entry vs the last
+  // kept one (kept entries form a prefix)
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (act[i]) {
+      sm.buf.x.q[4 * tid + i] = q[i];
+      sm.buf.x.i_ord[4 * tid + i] = kept[i] ? 1 : 0;
+    }
+  __syncthreads();
+  bool split = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = 4 * tid + i;
+    if (act[i] && !kept[i] && q[i] > 0.0f && k > 0)
+      split = split || (sm.buf.x.i_ord[k - 1] != 0 && sm.buf.x.q[k - 1] == q[i]);
+  }
+  double s2loc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s2loc[i] = s2;
+    s2 = s2 + (double)qk[i];
+  }
+  double S2;
+  const double base2 = big_excl_scan(s2, S2, sm);
+  const double t = (double)sm.uval * S2;  // draw (:447-459)
+  const double err2 = exact ? 0.0 : (8.0 * Kd * 0x1p-53 * S2 + 0x1p-50 * t);
+  int pos = 0x7FFFFFFF;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const double C2 = base2 + s2loc[i] + (double)qk[i];
+    if (kept[i] && C2 > t && pos == 0x7FFFFFFF) pos = 4 * tid + i;
+    near = near || (kept[i] && err2 > 0.0 && fabs(C2 - t) <= err2);
+  }
+  if (tid == 0) sm.pos = 0x7FFFFFFF;
+  __syncthreads();
+  if (pos != 0x7FFFFFFF) atomicMin(&sm.pos, pos);
+  const uint32_t ambm = block_or_u32((near ? 1u : 0u) | (split ? 2u : 0u), sm);
+  const int ps = sm.pos;
+  bool amb = !elig || ambm != 0u || ps == 0x7FFFFFFF;
+  if (!amb) {  // the draw must not land inside a group of equal q
+    const float qp = sm.buf.x.q[ps];
+    amb = (ps > 0 && sm.buf.x.q[ps - 1] == qp) || (ps + 1 < K && sm.buf.x.q[ps + 1] == qp);
+  }
+  if (amb) {
+    if (tid == 0) sm.replay = 1;
+    __syncthreads();
+    return;
+  }
+  if (tid == 0) {
+    sm.token = (int32_t)(~(uint32_t)sm.topkey[ps]);
+    sm.rowflags = kRowTopkFast;
+    sm.replay = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (act[i]) {
+      const int64_t o = (int64_t)row * p.out.topk_stride + 4 * tid + i;
+      if (p.out.topk_idx) p.out.topk_idx[o] = id[i];
+      if (p.out.topk_prob) p.out.topk_prob[o] = (float)((double)qk[i] / S2);
+    }
+  }
+  __syncthreads();
+}
+
+// ---- exact path for large K ----------------------------------------------------
+// The min-buffer (Sampler.pas:341-383) as a two-level tournament: leaf[s]
+// (LDS) is slot s's entry, slot_key << 32 | index; wave 0's lane g holds the
+// smallest (key << 32 | slot) of leaves 64g .. 64g + 63, so the smallest of
+// the lanes is the reference's first strict minimum (smallest value, then
+// lowest slot; NaN sorts above +inf).  An entering logit replaces that leaf,
+// and its group and the top are reduced again.
+struct TourBuf {
+  uint64_t g;
+  uint32_t mkey;
+  uint32_t mslot;
+};
+__device__ __forceinline__ uint64_t tb_group_min(const TopkBigSmem &sm, int K, int gi) {
+  const int s = gi * 64 + lane_id();
+  const uint64_t e = (s < K) ? ((sm.buf.x.leaf[s] & 0xFFFFFFFF00000000ull) | (uint32_t)s) : ~0ull;
+  return wave_min_u64(e);
+}
+__device__ __forceinline__ void tb_refresh(TourBuf &t, int G) {
+  const uint64_t m = wave_min_u64(lane_id() < G ? t.g : ~0ull);
+  t.mkey = (uint32_t)(m >> 32);
+  t.mslot = (uint32_t)m;
+}
+__device__ __forceinline__ void tb_enter(TourBuf &t, TopkBigSmem &sm, int K, int G, uint32_t xk, uint32_t xi) {
+  const int s = (int)t.mslot;
+  if (lane_id() == 0) sm.buf.x.leaf[s] = ((uint64_t)xk << 32) | xi;  // read back below by the same wave
+  const int gi = s >> 6;
+  const uint64_t gm = tb_group_min(sm, K, gi);
+  if (lane_id() == gi) t.g = gm;
+  tb_refresh(t, G);
+}
+__device__ __forceinline__ void tb_feed(TourBuf &t, TopkBigSmem &sm, int K, int G, bool has, uint32_t ck,
+                                        uint32_t ci) {
+  uint64_t pend = __ballot(has && ck > t.mkey);
+  while (pend) {
+    const int src = __ffsll((unsigned long long)pend) - 1;
+    tb_enter(t, sm, K, G, readlane32(ck, src), readlane32(ci, src));
+    pend &= ~(1ull << src);
+    pend &= __ballot(ck > t.mkey);
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, TopkBigSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int K = p.top_k, V = p.vocab, S = p.nchunks;
+  const int G = (K + 63) >> 6;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const bool pen = p.fuse_penalty != 0;
+  TourBuf tb{~0ull, 0xFFFFFFFFu, 0u};
+  uint64_t *list = sm.buf.x.list;
+  float v[kPerThread];
+  for (int c = 0; c < S; ++c) {
+    const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+    __syncthreads();
+    if (c > 0 && sm.xfrozen) break;
+    reload_chunk<VEC>(L, c0, clen, pen, v);
+    if (c == 0) {
+      // the first K logits fill slots 0..K-1 (Sampler.pas:352-366); all lie in
+      // the chunk's first 1024-logit group (K <= 1024)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int s = wv * 256 + lane * 4 + e;
+        if (s < K) sm.buf.x.leaf[s] = ((uint64_t)slot_key(v[e]) << 32) | (uint32_t)s;
+      }
+      __syncthreads();
+      if (wv == 0) {
+        for (int gi = 0; gi < G; ++gi) {
+          const uint64_t gm = tb_group_min(sm, K, gi);
+          if (lane == gi) tb.g = gm;
+        }
+        tb_refresh(tb, G);
+        const float l0 = __uint_as_float(readlane32(__float_as_uint(v[0]), 0));
+        if (lane == 0) {
+          sm.xfrozen = (l0 != l0) ? 1 : 0;
+          sm.xmkey = tb.mkey;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      __syncthreads();
+      if (sm.xfrozen) break;
+      const uint32_t m = sm.xmkey;
+      const int base = j * 1024 + wv * 256 + lane * 4;
+      uint32_t bits = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = v[4 * j + e];
+        const int loc = base + e;
+        const bool ok = loc < clen && (c0 + loc) >= K && x == x && ord_key(x) > m;
+        bits |= ok ? (1u << e) : 0u;
+      }
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wave_incl_scan_u32(cnt);
+      if (lane == 63) sm.xw[wv] = incl;
+      __syncthreads();
+      uint32_t off = incl - cnt, total = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        off += (w < wv) ? sm.xw[w] : 0u;
+        total += sm.xw[w];
+      }
+      if (total == 0u) continue;  // uniform
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((bits >> e) & 1u) list[off++] = ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(c0 + base + e);
+      __syncthreads();
+      if (wv == 0) {
+        for (uint32_t g = 0u; g < total; g += 64u) {
+          const bool has = g + (uint32_t)lane < total;
+          const uint64_t en = has ? list[g + lane] : 0ull;
+          tb_feed(tb, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
+        }
+        if (lane == 0) sm.xmkey = tb.mkey;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- slot-order finish (Sampler.pas:385-459), literally ----
+  const bool frozen = sm.xfrozen != 0;
+  float mloc = __builtin_nanf("");
+  for (int s = tid; s < K; s += kBlock) {  // v_ord[] holds the buffer's values by slot
+    const uint32_t key = (uint32_t)(sm.buf.x.leaf[s] >> 32);
+    const float x = (key == 0xFFFFFFFFu) ? __builtin_nanf("") : key_float(key);
+    sm.buf.x.v_ord[s] = x;
+    mloc = fmaxf(mloc, x);  // NaN-ignoring
+  }
+  mloc = wave_max_f32(mloc);
+  __syncthreads();
+  if (lane == 0) sm.wfmax[wv] = mloc;
+  __syncthreads();
+  // M (strict '>' from L[0]): NaN when L[0] is NaN, else the largest
+  // non-NaN logit, which is in the buffer
+  const float M = frozen ? __builtin_nanf("")
+                         : fmaxf(fmaxf(sm.wfmax[0], sm.wfmax[1]), fmaxf(sm.wfmax[2], sm.wfmax[3]));
+  uint32_t qn = 0u;
+  for (int s = tid; s < K; s += kBlock) {
+    const float q = (float)exp(((double)sm.buf.x.v_ord[s] - (double)M) * (double)p.inv_t);
+    sm.buf.x.q[s] = q;
+    qn |= (q != q) ? 1u : 0u;
+  }
+  const bool qnan = block_or_u32(qn, sm) != 0u;
+  // sums and Min-P in slot order (:386-410)
+  if (tid == 0) {
+    double S = 0.0;
+    for (int k = 0; k < K; ++k) S = S + (double)sm.buf.x.q[k];
+    if (p.min_p > 0.0f) {
+      float best = sm.buf.x.q[0];
+      for (int k = 1; k < K; ++k)
+        if (sm.buf.x.q[k] > best) best = sm.buf.x.q[k];
+      const float thr = best * p.min_p;
+      S = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (sm.buf.x.q[k] < thr)
+          sm.buf.x.q[k] = 0.0f;
+        else
+          S = S + (double)sm.buf.x.q[k];
+      }
+    }
+    sm.S = S;
+  }
+  __syncthreads();
+  // draw order: the stable descending sort of Top-P (:412-429), else slot order;
+  // list[] then holds, per position, the slot it draws from
+  int N = 1;
+  while (N < K) N <<= 1;
+  if (p.top_p < 1.0f && !qnan) {
+    for (int s = tid; s < N; s += kBlock)
+      list[s] = (s < K) ? (((uint64_t)__float_as_uint(sm.buf.x.q[s]) << 32) | (0xFFFFFFFFu - (uint32_t)s)) : 0ull;
+    __syncthreads();
+    block_sort_desc(list, N);  // q descending, equal q in slot order (q >= 0: its bits order it)
+    for (int r = tid; r < K; r += kBlock) list[r] = 0xFFFFFFFFu - (uint32_t)list[r];
+    __syncthreads();
+  } else if (p.top_p < 1.0f) {
+    if (tid == 0) {  // NaN among q: the reference's insertion sort, literally
+      for (int r = 0; r < K; ++r) list[r] = (uint64_t)r;
+      for (int i = 1; i < K; ++i) {
+        const uint64_t si = list[i];
+        const float qv = sm.buf.x.q[si];
+        int j = i - 1;
+        while (j >= 0 && sm.buf.x.q[list[j]] < qv) {
+          list[j + 1] = list[j];
+          --j;
+        }
+        list[j + 1] = si;
+      }
+    }
+    __syncthreads();
+  } else {
+    for (int r = tid; r < K; r += kBlock) list[r] = (uint64_t)r;
+    __syncthreads();
+  }
+  for (int r = tid; r < K; r += kBlock) {
+    const int s = (int)list[r];
+    sm.buf.x.q_ord[r] = sm.buf.x.q[s];
+    sm.buf.x.i_ord[r] = (int32_t)((uint32_t)sm.buf.x.leaf[s] & kXbIdxMask);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double S = sm.S;
+    if (p.top_p < 1.0f) {  // Top-P cut (:431-444)
+      const double target = (double)p.top_p * S;
+      double C = 0.0;
+      S = 0.0;
+      for (int r = 0; r < K; ++r) {
+        if (C < target && sm.buf.x.q_ord[r] > 0.0f) {
+          C = C + (double)sm.buf.x.q_ord[r];
+          S = S + (double)sm.buf.x.q_ord[r];
+        } else {
+          sm.buf.x.q_ord[r] = 0.0f;
+        }
+      }
+    }
+    const double t = (double)sm.uval * S;  // draw (:447-459)
+    double C = 0.0;
+    int32_t tok = sm.buf.x.i_ord[K - 1];
+    uint32_t fl = kRowTopkReplay | kRowFallback;
+    for (int r = 0; r < K; ++r) {
+      C = C + (double)sm.buf.x.q_ord[r];
+      if (C > t) {
+        tok = sm.buf.x.i_ord[r];
+        fl = kRowTopkReplay;
+        break;
+      }
+    }
+    if (qnan || !(M == M)) fl |= kRowNan;
+    sm.token = tok;
+    sm.rowflags = fl;
+    sm.S = S;
+  }
+  __syncthreads();
+  if (p.out.topk_idx || p.out.topk_prob) {
+    // canonical order: value descending, then lower index (NaN first)
+    for (int r = tid; r < N; r += kBlock) {
+      uint64_t key = 0ull;
+      if (r < K) {
+        const int s = (int)list[r];
+        key = ((uint64_t)slot_key(sm.buf.x.v_ord[s]) << 32) |
+              ((uint64_t)(kXbIdxMask - (uint32_t)sm.buf.x.i_ord[r]) << 10) | (uint32_t)r;
+      }
+      sm.buf.x.leaf[r] = key;  // the buffer's leaves are no longer read
+    }
+    __syncthreads();
+    block_sort_desc(sm.buf.x.leaf, N);
+    for (int j = tid; j < K; j += kBlock) {
+      const int r = (int)(sm.buf.x.leaf[j] & 1023u);
+      const int64_t o = (int64_t)row * p.out.topk_stride + j;
+      if (p.out.topk_idx) p.out.topk_idx[o] = sm.buf.x.i_ord[r];
+      if (p.out.topk_prob)
+        p.out.topk_prob[o] = (sm.S > 0.0) ? (float)((double)sm.buf.x.q_ord[r] / sm.S) : 0.0f;
+    }
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_body_big(const CallParams &p0) {
+  __shared__ TopkBigSmem sm;
+  int row, chunk;
+  block_row_chunk(p0.nchunks, p0.rows, row, chunk);
+  if (!row_on_path(p0, row, 1)) return;
+  const CallParams p = for_row(p0, row);
+  const int S = p.nchunks, K = p.top_k, ccap = p.cand_cap;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const int c0 = chunk * kChunk;
+  const int clen = min(kChunk, p.vocab - c0);
+  ChunkMeta *cm = p.meta + (int64_t)row * S;
+  Cand *cr = p.cand + (int64_t)row * S * ccap;
+  RngPre rp = rng_prefetch(p.rng, row);
+  PenaltyPrefetch pf;
+  if (p.fuse_penalty) {
+    penalty_prefetch(p, row, pf);
+    penalty_clear(sm);
+  }
+  topk_stream<VEC>(p, row, L, c0, clen, big_chunk_quota(K, S), cr + (int64_t)chunk * ccap, cm + chunk, pf, sm,
+                   ccap);
+  if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
+  if (threadIdx.x == 0) {
+    sm.uval = rng_draw(p.rng, row, rp);
+    sm.replay = 1;
+  }
+  __syncthreads();
+  if (topk_merge_big<VEC>(p, L, S, cm, cr, ccap, sm)) topk_finish_big(p, row, sm);
+  __syncthreads();
+  if (sm.replay) topk_exact_big<VEC>(p, row, sm);
+  if (threadIdx.x == 0) {
+    p.out.tokens[row] = sm.token;
+    if (p.out.flags) p.out.flags[row] = sm.rowflags;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_topk_big_vec(CallParams p) { topk_body_big<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_big_scalar(CallParams p) { topk_body_big<false>(p); }
 
 // 16-byte aligned rows: four workgroups per CU (<= 128 VGPRs, no spills).
 __global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true>(p); }
@@ -2210,10 +3045,16 @@ hipError_t launch_greedy(const CallParams &p, hipStream_t st) {
 }
 
 hipError_t launch_topk(const CallParams &p, hipStream_t st) {
-  if (p.vec)
+  if (p.cand_cap > kCandCap) {  // some row has 64 < K <= kKBig
+    if (p.vec)
+      hipLaunchKernelGGL(k_topk_big_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+    else
+      hipLaunchKernelGGL(k_topk_big_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  } else if (p.vec) {
     hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
-  else
+  } else {
     hipLaunchKernelGGL(k_topk_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  }
   return hipGetLastError();
 }
 
