@@ -35,7 +35,8 @@ extern "C" {
 /* Per-row diagnostic flags written to vdx_sample_outputs.flags. */
 #define VDX_ROW_GREEDY 0x1
 #define VDX_ROW_TOPK_FAST 0x2     /* exact top-K without slot-order replay   */
-#define VDX_ROW_TOPK_REPLAY 0x4   /* exact reference min-buffer replay       */
+#define VDX_ROW_TOPK_REPLAY 0x4   /* exact path: the reference's min-buffer
+                                     replayed over the logits that enter it */
 #define VDX_ROW_FULL 0x8          /* K <= 0 or K >= V full-softmax path      */
 #define VDX_ROW_NAN 0x10          /* row held NaN (or inf) handled literally */
 #define VDX_ROW_FALLBACK 0x20     /* no cumulative weight exceeded t         */
@@ -113,8 +114,10 @@ int32_t vdx_sampler_process(vdx_sampler *s, float *logits, int32_t vocab);
  * repetition penalty exactly as Sampler.pas:285-303).  `uniforms` (device,
  * nullable) injects the per-row uniform in [0,1) that replaces the RNG draw
  * (the RNG is then not advanced); NULL draws from the sampler's RNG.
+ * Every 0 < TopK < V takes the reference's top-K path (Sampler.pas:327-460);
+ * TopK > 1024 runs one workgroup per row and is much slower.
  * Stream-ordered and asynchronous; allocates nothing once the workspace
- * covers `vocab`.  Rows must not alias. */
+ * covers `vocab` and TopK.  Rows must not alias. */
 int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows,
                                int32_t vocab, int64_t row_stride,
                                const float *uniforms,

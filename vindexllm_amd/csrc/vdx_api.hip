@@ -45,6 +45,10 @@ struct vdx_sampler {
   // workspace (sized for ws_chunks chunks per row, ws_cap candidate slots per chunk)
   int32_t ws_chunks = 0;
   int32_t ws_cap = 0;
+  // rows with K > kKBig: huge_rows rows of huge_rb bytes (slots and sort space)
+  uint8_t *d_huge = nullptr;
+  int32_t huge_rows = 0;
+  int64_t huge_rb = 0;
   ChunkMeta *d_meta = nullptr;
   Cand *d_cand = nullptr;
   FullMeta *d_fmeta = nullptr;
@@ -272,6 +276,25 @@ static unsigned char *scratch_on_current_device() {
   return g_scratch_ptr[dev];
 }
 
+// The per-row workspace of rows with K > kKBig, grown (outside the sampling
+// call's kernels) when more rows or a larger K are first seen.
+static int ensure_huge(vdx_sampler *s, int32_t rows, int32_t K) {
+  const int64_t rb = topk_huge_row_bytes(K);
+  if (rows <= s->huge_rows && rb <= s->huge_rb) return VDX_OK;
+  HIP_TRY(s, hipStreamSynchronize(s->stream));
+  HIP_TRY(s, hipDeviceSynchronize());
+  (void)hipFree(s->d_huge);
+  s->d_huge = nullptr;
+  const int32_t nr = rows > s->huge_rows ? rows : s->huge_rows;
+  const int64_t nb = rb > s->huge_rb ? rb : s->huge_rb;
+  s->huge_rows = 0;
+  s->huge_rb = 0;
+  HIP_TRY(s, hipMalloc(&s->d_huge, (size_t)nr * (size_t)nb));
+  s->huge_rows = nr;
+  s->huge_rb = nb;
+  return VDX_OK;
+}
+
 extern "C" {
 
 const char *vdx_sampler_version(void) { return "vdxsampler 0.1.0 (gfx950)"; }
@@ -305,6 +328,7 @@ void vdx_sampler_destroy(vdx_sampler *s) {
   (void)hipFree(s->d_cand);
   (void)hipFree(s->d_fmeta);
   (void)hipFree(s->d_gpart);
+  (void)hipFree(s->d_huge);
   (void)hipFree(s->d_tickets);
   (void)hipFree(s->d_row);
   (void)hipFree(s->d_lm);
@@ -483,13 +507,15 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
     return fail(s, VDX_E_INVALID_ARG, "process_device: need vocab > 0 and row_stride >= vocab");
   const vdx_sampler_config &c = s->cfg;
   // the paths this call takes (with per-row configs: any of the rows')
-  bool path_any[3] = {false, false, false};
+  bool path_any[4] = {false, false, false, false};
   bool pen_fused = false, pen_sep = false, full_minp = false;
-  int32_t kmax = 0;
+  int32_t kmax = 0, kmax_huge = 0;
   if (!s->per_row) {
     const RowCfg rc = row_params(c);
-    path_any[row_path(rc, vocab)] = true;
-    kmax = rc.top_k;
+    const int path = row_path(rc, vocab);
+    path_any[path] = true;
+    if (path == kPathTopk) kmax = rc.top_k;
+    if (path == kPathTopkHuge) kmax_huge = rc.top_k;
     pen_fused = row_fuses_penalty(rc, vocab);
     pen_sep = rc.penalty != 1.0f && !pen_fused;
     full_minp = rc.min_p > 0.0f;
@@ -498,16 +524,15 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
       const RowCfg rc = row_params(s->row_cfg[r]);
       const int path = row_path(rc, vocab);
       path_any[path] = true;
-      if (path == 1 && rc.top_k > kmax) kmax = rc.top_k;
+      if (path == kPathTopk && rc.top_k > kmax) kmax = rc.top_k;
+      if (path == kPathTopkHuge && rc.top_k > kmax_huge) kmax_huge = rc.top_k;
       if (rc.penalty != 1.0f) (row_fuses_penalty(rc, vocab) ? pen_fused : pen_sep) = true;
       if (path == 2 && rc.min_p > 0.0f) full_minp = true;
     }
   }
-  const bool topk = path_any[1];
-  if ((out->topk_idx || out->topk_prob) && topk && out->topk_stride < kmax)
+  const bool topk = path_any[kPathTopk], huge = path_any[kPathTopkHuge];
+  if ((out->topk_idx || out->topk_prob) && (topk || huge) && out->topk_stride < (kmax > kmax_huge ? kmax : kmax_huge))
     return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= TopK");
-  if (topk && kmax > kKBig)
-    return fail(s, VDX_E_UNSUPPORTED, "process_device: TopK > 1024 is not implemented on the GPU");
   if (chunks_for(vocab) > kMaxChunks)
     return fail(s, VDX_E_UNSUPPORTED, "process_device: vocab > 4194304 is not supported");
   // TopK > 64 runs the large-K kernel, with more candidate slots per chunk
@@ -515,6 +540,7 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   HIP_TRY(s, hipSetDevice(s->device));
   int rc = ensure_workspace(s, vocab, cap);
   if (rc != VDX_OK) return rc;
+  if (huge && (rc = ensure_huge(s, rows, kmax_huge)) != VDX_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
 
   CallParams p{};
@@ -538,13 +564,15 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.rng.kind = s->rng_kind;
   p.rng.u_out = out->uniforms;
   p.out.tokens = out->tokens;
-  p.out.topk_idx = topk ? out->topk_idx : nullptr;
-  p.out.topk_prob = topk ? out->topk_prob : nullptr;
+  p.out.topk_idx = (topk || huge) ? out->topk_idx : nullptr;
+  p.out.topk_prob = (topk || huge) ? out->topk_prob : nullptr;
   p.out.topk_stride = out->topk_stride;
   p.out.flags = out->flags;
   p.meta = s->d_meta;
   p.cand = s->d_cand;
   p.cand_cap = cap;
+  p.huge_ws = s->d_huge;
+  p.huge_row_bytes = s->huge_rb;
   p.fmeta = s->d_fmeta;
   p.gpart = s->d_gpart;
   p.tickets = s->d_tickets;
@@ -561,8 +589,10 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
   if (hist && pen_sep) HIP_TRY(s, launch_penalty(p, st));
   if (timed) HIP_TRY(s, hipEventRecord(ev[1], st));
+  // rows with K > kKBig: one workgroup each, on the call's stream
+  if (huge) HIP_TRY(s, launch_topk_huge(p, st));
   const int npaths = (int)path_any[0] + (int)path_any[1] + (int)path_any[2];
-  if (npaths == 1 || !s->aux[0]) {
+  if (npaths <= 1 || !s->aux[0]) {
     if (path_any[0]) HIP_TRY(s, launch_greedy(p, st));
     if (path_any[1]) HIP_TRY(s, launch_topk(p, st));
     if (path_any[2]) HIP_TRY(s, launch_full(p, st));
@@ -609,7 +639,8 @@ int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int3
     return bad(VDX_E_UNSUPPORTED, "noalloc: rows * ceil(vocab / 16384) must be <= 4096 and rows <= 1024 "
                                   "(the fixed workspace)");
   if (S > kMaxChunks) return bad(VDX_E_UNSUPPORTED, "noalloc: vocab > 4194304 is not supported");
-  if (path == 1 && rc.top_k > kKMax) return bad(VDX_E_UNSUPPORTED, "noalloc: TopK > 64 is not implemented");
+  if ((path == kPathTopk && rc.top_k > kKMax) || path == kPathTopkHuge)
+    return bad(VDX_E_UNSUPPORTED, "noalloc: TopK > 64 is not supported by this entry point");
   if ((out->topk_idx || out->topk_prob) && path == 1 && out->topk_stride < rc.top_k)
     return bad(VDX_E_INVALID_ARG, "noalloc: topk_stride must be >= TopK");
   const int32_t window = rc.window;

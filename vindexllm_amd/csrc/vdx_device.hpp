@@ -48,15 +48,19 @@ struct RowCfg {
 };
 
 // Sampling path of a row over V logits (Sampler.pas:305, 327, 461):
-// 0 greedy, 1 top-K, 2 full softmax.
+// 0 greedy, 1 top-K with K <= kKBig, 2 full softmax, 3 top-K with K > kKBig
+// (one workgroup per row, exact replay only).
+constexpr int kPathGreedy = 0, kPathTopk = 1, kPathFull = 2, kPathTopkHuge = 3;
 __host__ __device__ __forceinline__ int row_path(const RowCfg &c, int V) {
-  return c.greedy ? 0 : ((c.top_k > 0 && c.top_k < V) ? 1 : 2);
+  if (c.greedy) return kPathGreedy;
+  if (c.top_k > 0 && c.top_k < V) return c.top_k <= kKBig ? kPathTopk : kPathTopkHuge;
+  return kPathFull;
 }
 // The sampling kernel applies this row's penalty itself (its window fits the
-// kernels' history table); rows with longer windows take the separate kernel.
+// kernels' history table); rows with longer windows, and rows of the K > kKBig
+// kernel (which has no stream phase), take the separate kernel.
 __host__ __device__ __forceinline__ bool row_fuses_penalty(const RowCfg &c, int V) {
-  (void)V;
-  return c.penalty != 1.0f && c.window <= kPenMax;
+  return c.penalty != 1.0f && c.window <= kPenMax && row_path(c, V) != kPathTopkHuge;
 }
 
 // Per-chunk candidate quota of the top-K stream phase.  A chunk stores every

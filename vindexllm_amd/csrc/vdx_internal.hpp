@@ -31,6 +31,8 @@ struct CallParams {
   ChunkMeta *meta;
   Cand *cand;
   int32_t cand_cap;     // candidate slots per chunk: kCandCap, or more when some row has K > 64
+  uint8_t *huge_ws;     // rows with K > kKBig: per-row slots and sort space
+  int64_t huge_row_bytes;
   FullMeta *fmeta;
   uint64_t *gpart;
   uint32_t *tickets;
@@ -66,6 +68,9 @@ hipError_t launch_penalty(const CallParams &p, hipStream_t st);
 hipError_t launch_greedy(const CallParams &p, hipStream_t st);
 hipError_t launch_topk(const CallParams &p, hipStream_t st);
 hipError_t launch_full(const CallParams &p, hipStream_t st);
+// Rows with K > kKBig (one workgroup per row) and the workspace each needs.
+hipError_t launch_topk_huge(const CallParams &p, hipStream_t st);
+int64_t topk_huge_row_bytes(int K);
 hipError_t launch_hist_gather(const int32_t *hist_row, int32_t slots, const RowState *rs_row, const float *L,
                               int32_t vocab, uint64_t *out, hipStream_t st);
 hipError_t launch_hist_add(const int32_t *tokens, int32_t tok_const, int32_t row0,

@@ -455,7 +455,7 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p0) {
   __shared__ PenaltySmem ps;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
-  if (!row_on_path(p0, row, 0)) return;
+  if (!row_on_path(p0, row, kPathGreedy)) return;
   const CallParams p = for_row(p0, row);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -1795,7 +1795,7 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
   __shared__ TopkSmem sm;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
-  if (!row_on_path(p0, row, 1)) return;
+  if (!row_on_path(p0, row, kPathTopk)) return;
   const CallParams p = for_row(p0, row);
   const int S = p.nchunks, K = p.top_k;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -2535,7 +2535,7 @@ __device__ __forceinline__ void topk_body_big(const CallParams &p0) {
   __shared__ TopkBigSmem sm;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
-  if (!row_on_path(p0, row, 1)) return;
+  if (!row_on_path(p0, row, kPathTopk)) return;
   const CallParams p = for_row(p0, row);
   const int S = p.nchunks, K = p.top_k, ccap = p.cand_cap;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -2568,6 +2568,359 @@ __device__ __forceinline__ void topk_body_big(const CallParams &p0) {
 
 __global__ __launch_bounds__(kBlock) void k_topk_big_vec(CallParams p) { topk_body_big<true>(p); }
 __global__ __launch_bounds__(kBlock) void k_topk_big_scalar(CallParams p) { topk_body_big<false>(p); }
+
+// =============================================================================
+// Top-K for K > kKBig (Sampler.pas:327-460): one workgroup per row replays
+// the min-buffer exactly -- every chunk re-read, only logits above the
+// buffer's minimum fed, the K slots in a per-row HBM workspace under a
+// three-level tournament -- and finishes in slot order literally, with the
+// Top-P order and the canonical output order sorted in HBM.  Slow but exact;
+// the reference's own scan costs K per entering logit.
+// =============================================================================
+struct HugeView {
+  uint64_t *leaf;   // [K] slot s: slot_key << 32 | index
+  uint64_t *l1;     // [ceil(K/64)] minimum (key << 32 | slot) of 64 leaves
+  float *q;         // [K] by slot
+  float *q_ord;     // [K] by draw position
+  int32_t *i_ord;   // [K] by draw position
+  uint64_t *keys;   // [N] sort keys (N = the power of two >= K)
+  uint32_t *vals;   // [N] sort payloads
+};
+__host__ __device__ __forceinline__ int64_t huge_align(int64_t x) { return (x + 255) & ~(int64_t)255; }
+__host__ __device__ __forceinline__ int64_t huge_row_bytes(int K) {
+  int64_t N = 1;
+  while (N < K) N <<= 1;
+  const int64_t G1 = (K + 63) / 64;
+  return huge_align(8 * (int64_t)K) + huge_align(8 * G1) + 2 * huge_align(4 * (int64_t)K) +
+         huge_align(4 * (int64_t)K) + huge_align(8 * N) + huge_align(4 * N);
+}
+__device__ __forceinline__ HugeView huge_view(const CallParams &p, int row, int K) {
+  uint8_t *b = p.huge_ws + (int64_t)row * p.huge_row_bytes;
+  int64_t N = 1;
+  while (N < K) N <<= 1;
+  const int64_t G1 = (K + 63) / 64;
+  HugeView h;
+  h.leaf = reinterpret_cast<uint64_t *>(b);
+  b += huge_align(8 * (int64_t)K);
+  h.l1 = reinterpret_cast<uint64_t *>(b);
+  b += huge_align(8 * G1);
+  h.q = reinterpret_cast<float *>(b);
+  b += huge_align(4 * (int64_t)K);
+  h.q_ord = reinterpret_cast<float *>(b);
+  b += huge_align(4 * (int64_t)K);
+  h.i_ord = reinterpret_cast<int32_t *>(b);
+  b += huge_align(4 * (int64_t)K);
+  h.keys = reinterpret_cast<uint64_t *>(b);
+  b += huge_align(8 * N);
+  h.vals = reinterpret_cast<uint32_t *>(b);
+  return h;
+}
+
+constexpr int kHugeL2 = 1024;  // 64-group minima of the 64-leaf group minima: K <= 4 Mi
+struct TopkHugeSmem {
+  uint64_t l2[kHugeL2];
+  uint64_t list[1024];
+  uint32_t xw[kWaves];
+  uint32_t xmkey;
+  int32_t xfrozen;
+  float wfmax[kWaves];
+  double S;
+  float uval;
+  int32_t token;
+  uint32_t rowflags;
+};
+
+// Descending bitonic sort of keys[0, N) (HBM) carrying vals[], whole workgroup.
+__device__ __forceinline__ void hbm_sort_desc(uint64_t *keys, uint32_t *vals, int64_t N) {
+  for (int64_t k2 = 2; k2 <= N; k2 <<= 1) {
+    for (int64_t j = k2 >> 1; j > 0; j >>= 1) {
+      for (int64_t i = threadIdx.x; i < N; i += kBlock) {
+        const int64_t ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = keys[i], y = keys[ixj];
+          const bool desc = (i & k2) == 0;
+          if ((x < y) == desc) {
+            keys[i] = y;
+            keys[ixj] = x;
+            if (vals) {
+              const uint32_t a = vals[i];
+              vals[i] = vals[ixj];
+              vals[ixj] = a;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Wave 0: the minimum (key << 32 | slot) of leaves 64g .. 64g+63, with leaf
+// s = `ps` read as `pv` (just written by this wave).
+__device__ __forceinline__ uint64_t hg_group(const HugeView &h, int K, int g, int ps, uint64_t pv) {
+  const int s = 64 * g + lane_id();
+  uint64_t e = ~0ull;
+  if (s < K) e = (((s == ps) ? pv : h.leaf[s]) & 0xFFFFFFFF00000000ull) | (uint32_t)s;
+  return wave_min_u64(e);
+}
+__device__ __forceinline__ uint64_t hg_super(const HugeView &h, int G1, int hh, int pg, uint64_t pv) {
+  const int g = 64 * hh + lane_id();
+  uint64_t e = ~0ull;
+  if (g < G1) e = (g == pg) ? pv : h.l1[g];
+  return wave_min_u64(e);
+}
+__device__ __forceinline__ void hg_top(const TopkHugeSmem &sm, int G2, uint32_t &mkey, uint32_t &mslot) {
+  uint64_t m = ~0ull;
+  for (int i = lane_id(); i < G2; i += 64) m = sm.l2[i] < m ? sm.l2[i] : m;
+  m = wave_min_u64(m);
+  mkey = (uint32_t)(m >> 32);
+  mslot = (uint32_t)m;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_body_huge(const CallParams &p0) {
+  __shared__ TopkHugeSmem sm;
+  const int row = blockIdx.x;
+  if (!row_on_path(p0, row, kPathTopkHuge)) return;
+  const CallParams p = for_row(p0, row);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int K = p.top_k, V = p.vocab, S = p.nchunks;
+  const int G1 = (K + 63) / 64, G2 = (G1 + 63) / 64;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const HugeView h = huge_view(p, row, K);
+  RngPre rp = rng_prefetch(p.rng, row);
+  if (tid == 0) sm.uval = rng_draw(p.rng, row, rp);
+  uint32_t mkey = 0u, mslot = 0u;  // wave 0
+  float v[kPerThread];
+  const int cK = (K - 1) / kChunk;  // the chunk holding slot K-1
+  // the first K logits fill slots 0..K-1 (Sampler.pas:352-366)
+  for (int c = 0; c <= cK; ++c) {
+    const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+    reload_chunk<VEC>(L, c0, clen, false, v);
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int loc = chunk_pos(wv, lane, i), s = c0 + loc;
+      if (loc < clen && s < K) h.leaf[s] = ((uint64_t)slot_key(v[i]) << 32) | (uint32_t)s;
+    }
+  }
+  __syncthreads();
+  // the tournament: level 1 in HBM (each wave a share of the groups), level 2 in LDS
+  for (int g = wv; g < G1; g += kWaves) {
+    const uint64_t m = hg_group(h, K, g, -1, 0ull);
+    if (lane == 0) h.l1[g] = m;
+  }
+  __syncthreads();
+  for (int hh = wv; hh < G2; hh += kWaves) {
+    const uint64_t m = hg_super(h, G1, hh, -1, 0ull);
+    if (lane == 0) sm.l2[hh] = m;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    hg_top(sm, G2, mkey, mslot);
+    const float l0 = xloadf(&L[0]);
+    if (lane == 0) {
+      sm.xfrozen = (l0 != l0) ? 1 : 0;  // a NaN at index 0 stays the minimum (:369)
+      sm.xmkey = mkey;
+    }
+  }
+  // the walk: chunk cK onwards, logits above the minimum in index order
+  for (int c = cK; c < S; ++c) {
+    const int c0 = c * kChunk, clen = min(kChunk, V - c0);
+    __syncthreads();
+    if (sm.xfrozen) break;
+    reload_chunk<VEC>(L, c0, clen, false, v);
+#pragma unroll
+    for (int j = 0; j < kPerThread / 4; ++j) {
+      __syncthreads();
+      const uint32_t m = sm.xmkey;
+      const int base = j * 1024 + wv * 256 + lane * 4;
+      uint32_t bits = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = v[4 * j + e];
+        const int loc = base + e;
+        bits |= (loc < clen && (c0 + loc) >= K && x == x && ord_key(x) > m) ? (1u << e) : 0u;
+      }
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wave_incl_scan_u32(cnt);
+      if (lane == 63) sm.xw[wv] = incl;
+      __syncthreads();
+      uint32_t off = incl - cnt, total = 0u;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        off += (w < wv) ? sm.xw[w] : 0u;
+        total += sm.xw[w];
+      }
+      if (total == 0u) continue;  // uniform
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((bits >> e) & 1u) sm.list[off++] = ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(c0 + base + e);
+      __syncthreads();
+      if (wv == 0) {
+        for (uint32_t g0 = 0u; g0 < total; g0 += 64u) {
+          const bool has = g0 + (uint32_t)lane < total;
+          const uint64_t en = has ? sm.list[g0 + lane] : 0ull;
+          const uint32_t ck = (uint32_t)(en >> 32), ci = (uint32_t)en;
+          uint64_t pend = __ballot(has && ck > mkey);
+          while (pend) {
+            const int src = __ffsll((unsigned long long)pend) - 1;
+            // the logit takes the minimum's slot; its group, super-group and the top are reduced again
+            const int s = (int)mslot;
+            const uint64_t nv = ((uint64_t)readlane32(ck, src) << 32) | readlane32(ci, src);
+            if (lane == 0) h.leaf[s] = nv;
+            const int g = s >> 6;
+            const uint64_t gm = hg_group(h, K, g, s, nv);
+            if (lane == 0) h.l1[g] = gm;
+            const uint64_t sm2 = hg_super(h, G1, g >> 6, g, gm);
+            if (lane == 0) sm.l2[g >> 6] = sm2;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");  // HBM stores before later reads
+            hg_top(sm, G2, mkey, mslot);
+            pend &= ~(1ull << src);
+            pend &= __ballot(ck > mkey);
+          }
+        }
+        if (lane == 0) sm.xmkey = mkey;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- slot-order finish (Sampler.pas:385-459), literally ----
+  const bool frozen = sm.xfrozen != 0;
+  float mloc = __builtin_nanf("");
+  for (int s = tid; s < K; s += kBlock) {
+    const uint32_t key = (uint32_t)(h.leaf[s] >> 32);
+    mloc = fmaxf(mloc, (key == 0xFFFFFFFFu) ? __builtin_nanf("") : key_float(key));
+  }
+  mloc = wave_max_f32(mloc);
+  if (lane == 0) sm.wfmax[wv] = mloc;
+  __syncthreads();
+  const float M = frozen ? __builtin_nanf("")
+                         : fmaxf(fmaxf(sm.wfmax[0], sm.wfmax[1]), fmaxf(sm.wfmax[2], sm.wfmax[3]));
+  uint32_t qn = 0u;
+  for (int s = tid; s < K; s += kBlock) {
+    const uint32_t key = (uint32_t)(h.leaf[s] >> 32);
+    const float x = (key == 0xFFFFFFFFu) ? __builtin_nanf("") : key_float(key);
+    const float q = (float)exp(((double)x - (double)M) * (double)p.inv_t);
+    h.q[s] = q;
+    qn |= (q != q) ? 1u : 0u;
+  }
+  qn = wave_or_u32(qn);
+  __syncthreads();
+  if (lane == 0) sm.xw[wv] = qn;
+  __syncthreads();
+  const bool qnan = (sm.xw[0] | sm.xw[1] | sm.xw[2] | sm.xw[3]) != 0u;
+  if (tid == 0) {  // sums and Min-P in slot order (:386-410)
+    double Sv = 0.0;
+    for (int k = 0; k < K; ++k) Sv = Sv + (double)h.q[k];
+    if (p.min_p > 0.0f) {
+      float best = h.q[0];
+      for (int k = 1; k < K; ++k)
+        if (h.q[k] > best) best = h.q[k];
+      const float thr = best * p.min_p;
+      Sv = 0.0;
+      for (int k = 0; k < K; ++k) {
+        if (h.q[k] < thr)
+          h.q[k] = 0.0f;
+        else
+          Sv = Sv + (double)h.q[k];
+      }
+    }
+    sm.S = Sv;
+  }
+  __syncthreads();
+  int64_t N = 1;
+  while (N < K) N <<= 1;
+  // draw order in vals[]: the stable descending sort of Top-P (:412-429), else slot order
+  if (p.top_p < 1.0f && !qnan) {
+    for (int64_t s = tid; s < N; s += kBlock)
+      h.keys[s] = (s < K) ? (((uint64_t)__float_as_uint(h.q[s]) << 32) | (0xFFFFFFFFu - (uint32_t)s)) : 0ull;
+    __syncthreads();
+    hbm_sort_desc(h.keys, nullptr, N);
+    for (int r = tid; r < K; r += kBlock) h.vals[r] = 0xFFFFFFFFu - (uint32_t)h.keys[r];
+  } else if (p.top_p < 1.0f) {
+    if (tid == 0) {  // NaN among q: the reference's insertion sort, literally
+      for (int r = 0; r < K; ++r) h.vals[r] = (uint32_t)r;
+      for (int i = 1; i < K; ++i) {
+        const uint32_t si = h.vals[i];
+        const float qv = h.q[si];
+        int j = i - 1;
+        while (j >= 0 && h.q[h.vals[j]] < qv) {
+          h.vals[j + 1] = h.vals[j];
+          --j;
+        }
+        h.vals[j + 1] = si;
+      }
+    }
+  } else {
+    for (int r = tid; r < K; r += kBlock) h.vals[r] = (uint32_t)r;
+  }
+  __syncthreads();
+  for (int r = tid; r < K; r += kBlock) {
+    const uint32_t s = h.vals[r];
+    h.q_ord[r] = h.q[s];
+    h.i_ord[r] = (int32_t)((uint32_t)h.leaf[s] & kXbIdxMask);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double Sv = sm.S;
+    if (p.top_p < 1.0f) {  // Top-P cut (:431-444)
+      const double target = (double)p.top_p * Sv;
+      double C = 0.0;
+      Sv = 0.0;
+      for (int r = 0; r < K; ++r) {
+        if (C < target && h.q_ord[r] > 0.0f) {
+          C = C + (double)h.q_ord[r];
+          Sv = Sv + (double)h.q_ord[r];
+        } else {
+          h.q_ord[r] = 0.0f;
+        }
+      }
+    }
+    const double t = (double)sm.uval * Sv;  // draw (:447-459)
+    double C = 0.0;
+    int32_t tok = h.i_ord[K - 1];
+    uint32_t fl = kRowTopkReplay | kRowFallback;
+    for (int r = 0; r < K; ++r) {
+      C = C + (double)h.q_ord[r];
+      if (C > t) {
+        tok = h.i_ord[r];
+        fl = kRowTopkReplay;
+        break;
+      }
+    }
+    if (qnan || !(M == M)) fl |= kRowNan;
+    p.out.tokens[row] = tok;
+    if (p.out.flags) p.out.flags[row] = fl;
+    sm.S = Sv;
+  }
+  __syncthreads();
+  if (p.out.topk_idx || p.out.topk_prob) {
+    // canonical order: value descending, then lower index (NaN first)
+    for (int64_t r = tid; r < N; r += kBlock) {
+      uint64_t key = 0ull;
+      if (r < K) {
+        const uint32_t s = h.vals[r];
+        const uint32_t vk = (uint32_t)(h.leaf[s] >> 32);
+        key = ((uint64_t)vk << 32) | (kXbIdxMask - (uint32_t)h.i_ord[r]);
+      }
+      h.keys[r] = key;
+    }
+    __syncthreads();
+    for (int64_t r = tid; r < N; r += kBlock) h.vals[r] = (uint32_t)r;
+    __syncthreads();
+    hbm_sort_desc(h.keys, h.vals, N);
+    for (int j = tid; j < K; j += kBlock) {
+      const uint32_t r = h.vals[j];
+      const int64_t o = (int64_t)row * p.out.topk_stride + j;
+      if (p.out.topk_idx) p.out.topk_idx[o] = h.i_ord[r];
+      if (p.out.topk_prob) p.out.topk_prob[o] = (sm.S > 0.0) ? (float)((double)h.q_ord[r] / sm.S) : 0.0f;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_topk_huge_vec(CallParams p) { topk_body_huge<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_huge_scalar(CallParams p) { topk_body_huge<false>(p); }
 
 // 16-byte aligned rows: four workgroups per CU (<= 128 VGPRs, no spills).
 __global__ __launch_bounds__(kBlock, 4) void k_topk_vec(CallParams p) { topk_body<true>(p); }
@@ -2624,7 +2977,7 @@ __global__ __launch_bounds__(kBlock) void k_full_max(CallParams p0) {
   __shared__ PenaltySmem ps;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
-  if (!row_on_path(p0, row, 2)) return;
+  if (!row_on_path(p0, row, kPathFull)) return;
   const CallParams p = for_row(p0, row);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -2670,7 +3023,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   __shared__ FullSmem sm;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
-  if (!row_on_path(p0, row, 2)) return;
+  if (!row_on_path(p0, row, kPathFull)) return;
   const CallParams p = for_row(p0, row);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int S = p.nchunks, V = p.vocab;
@@ -3057,6 +3410,16 @@ hipError_t launch_topk(const CallParams &p, hipStream_t st) {
   }
   return hipGetLastError();
 }
+
+hipError_t launch_topk_huge(const CallParams &p, hipStream_t st) {
+  if (p.vec)
+    hipLaunchKernelGGL(k_topk_huge_vec, dim3(p.rows), dim3(kBlock), 0, st, p);
+  else
+    hipLaunchKernelGGL(k_topk_huge_scalar, dim3(p.rows), dim3(kBlock), 0, st, p);
+  return hipGetLastError();
+}
+
+int64_t topk_huge_row_bytes(int K) { return huge_row_bytes(K); }
 
 hipError_t launch_full(const CallParams &p, hipStream_t st) {
   const dim3 g = grid_rows_chunks(p);
