@@ -48,6 +48,7 @@ import numpy as np  # noqa: E402
 METRIC = "rows/sec sampled (B=64, V=262144, topk64/topp0.95); % of HBM peak"
 MIN_TIMED = 128          # fewest steps in a timed region
 NORTH_STAR = "topk_b256"  # B=256 top-k 64 / top-p 0.95: the >= 60% of HBM target
+EXTRA = ("topk128_b64", "topk_only_b64")
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 POOL_BYTES = 2 << 30
 
@@ -64,6 +65,14 @@ WORKLOADS = {
         rows=256, vocab=262144, hist=0,
         cfg=dict(Temperature=0.7, TopK=0, TopP=0.9, Seed=3004),
         desc="full-vocab B=256 V=262144 Zipf logits, T 0.7, top-k 0 (TopP ignored as in the reference)"),
+    "topk128_b64": dict(
+        rows=64, vocab=262144, hist=0,
+        cfg=dict(Temperature=1.0, TopK=128, TopP=0.95, Seed=3011),
+        desc="B=64 V=262144 3N(0,1)+8@16 ids, T 1.0, top-k 128, top-p 0.95 (large-K kernel)"),
+    "topk_only_b64": dict(
+        rows=64, vocab=262144, hist=0,
+        cfg=dict(Temperature=1.0, TopK=64, TopP=1.0, Seed=3012),
+        desc="B=64 V=262144 3N(0,1)+8@16 ids, T 1.0, top-k 64, top-p 1 (draw in slot order: exact path)"),
     "greedy_b64": dict(
         rows=64, vocab=262144, hist=0, cfg=dict(Temperature=0.0, Seed=3002),
         desc="greedy argmax B=64 V=262144, 4 tied maxima/row"),
@@ -82,6 +91,7 @@ WORKLOADS = {
              "top-k 40/min-p 0.05, full softmax; all penalised"),
 }
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
+                   "topk128_b64": "k_topk_big_vec", "topk_only_b64": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec", "mixed_rows_b64": "k_topk_vec"}
 
@@ -641,6 +651,20 @@ def main():
     }
     if "parity" in r:
         out["parity"] = r["parity"]
+    if not a.no_north_star:
+        # other top-K settings of the same shape: a larger K, and Top-P = 1 (slot-order draw)
+        extra = {}
+        for name in EXTRA:
+            if name == a.workload:
+                continue
+            o = run_gpu(name, MIN_TIMED, min(a.warmup, 20), a.eager, check=not a.no_check)
+            ob = o["step_bytes"] / (o["kernel_ms"] * 1e-3) / 1e9
+            extra[name] = {"workload": WORKLOADS[name]["desc"], "steps": o["steps"],
+                           "rows_per_s": o["rows"] * o["steps"] / o["elapsed"],
+                           "us_per_step": 1e6 * o["elapsed"] / o["steps"], "kernel_us": 1e3 * o["kernel_ms"],
+                           "hbm_frac": ob / HBM_PEAK_GBS, "rows_fast_path": o["fast_frac"],
+                           "rows_exact_path": o["replay_frac"], "parity": o.get("parity")}
+        out["extra_workloads"] = extra
     if NORTH_STAR != a.workload and not a.no_north_star:
         # the target shape: B=256 x V=262144 fp32, top-k 64 / top-p 0.95
         n = run_gpu(NORTH_STAR, steps, min(a.warmup, 20), a.eager, check=not a.no_check)

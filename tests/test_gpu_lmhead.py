@@ -106,13 +106,17 @@ def _cfg5(B, seed):
     return w, H, u, V, D
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("B", [1, 16])
-def test_cfg5_lmhead_plus_sampling(B):
+def test_cfg5_lmhead_plus_sampling(B, packed):
+    # the config-5 shape (262144 x 2560 Q4_0) in the GGUF layout and in the
+    # packed layout the benchmark times: logits bit-exact with the kernel-order
+    # restatement either way
     import torch
 
-    from vindexllm_amd import TVdxSampler
+    from vindexllm_amd import VDX_LMHEAD_PACKED, VDX_TENSOR_Q4_0, TVdxSampler, lmhead_pack
 
-    log(f"[case] C5 lm_head + top-k64/top-p0.95/T1 B={B}")
+    log(f"[case] C5 lm_head + top-k64/top-p0.95/T1 B={B} packed={packed}")
     w, H, u, V, D = _cfg5(B, 1005 + B)
     cfg = dict(temperature=1.0, top_k=64, top_p=0.95)
     dev = torch.device("cuda:0")
@@ -127,9 +131,15 @@ def test_cfg5_lmhead_plus_sampling(B):
         c.Temperature, c.TopK, c.TopP = 1.0, 64, 0.95
         s.SetConfig(c)
         ud = torch.from_numpy(u).to(dev)
-        tok = s.lmhead_q4_0_device(wd, hd, V, logits=L, uniforms=ud, topk_idx=ti, topk_prob=tp,
-                                   flags=fl)
-        tok2 = s.lmhead_q4_0_device(wd, hd, V, uniforms=ud)  # the sampler's own workspace
+        if packed:
+            wp = lmhead_pack(wd, VDX_TENSOR_Q4_0, D, V)
+            wt = VDX_TENSOR_Q4_0 | VDX_LMHEAD_PACKED
+            tok = s.lmhead_device(wp, wt, hd, V, logits=L, uniforms=ud, topk_idx=ti, topk_prob=tp, flags=fl)
+            tok2 = s.lmhead_device(wp, wt, hd, V, uniforms=ud)  # the sampler's own workspace
+        else:
+            tok = s.lmhead_q4_0_device(wd, hd, V, logits=L, uniforms=ud, topk_idx=ti, topk_prob=tp,
+                                       flags=fl)
+            tok2 = s.lmhead_q4_0_device(wd, hd, V, uniforms=ud)  # the sampler's own workspace
         torch.cuda.synchronize()
     Lg = L.cpu().numpy()
     g = dict(tokens=tok.cpu().numpy(), topk_idx=ti.cpu().numpy(), topk_prob=tp.cpu().numpy(),
@@ -157,7 +167,7 @@ def test_cfg5_lmhead_plus_sampling(B):
                 f"(logit err {err:.2e}, K-boundary gap {gap:.2e}, CDF distance {bd:.2e})")
             assert gap <= 4 * err or bd <= 1e-4, f"row {b}: unexplained token difference"
             flips += 1
-    log(f"[done] C5 B={B}: near-boundary draws {nb}, shader-order flips {flips}/{B}, "
+    log(f"[done] C5 B={B} packed={packed}: near-boundary draws {nb}, shader-order flips {flips}/{B}, "
         f"flags {sorted(set(g['flags'].tolist()))}")
 
 
