@@ -59,7 +59,9 @@ typedef struct vdx_sampler vdx_sampler;
 /* Optional outputs of vdx_sampler_process_device.  Every pointer is device
  * memory and may be NULL.  topk_* hold `topk_stride` entries per row (>= K)
  * in descending (value, then lower index) order; topk_prob is the final
- * normalised probability (0 for entries cut by Min-P / Top-P). */
+ * normalised probability (0 for entries cut by Min-P / Top-P).  A row of the
+ * full-softmax path (K <= 0 or K >= V) writes entry 0 only: the drawn token
+ * and its probability q / S (0 when the row's weights are not finite). */
 typedef struct vdx_sample_outputs {
   int32_t *tokens;     /* [rows]                    */
   int32_t *topk_idx;   /* [rows * topk_stride]      */

@@ -51,7 +51,7 @@ def gpu_sample(logits: np.ndarray, cfg: dict, u: np.ndarray | None, hist=None, t
         if hist is not None:
             for r in range(B):
                 s.set_history(r, hist[r])
-        K = max(int(c.TopK), 1)
+        K = min(max(int(c.TopK), 1), V)  # a full-softmax row (K <= 0 or K >= V) reports one entry
         ti = torch.full((B, K), -1, dtype=torch.int32, device=dev) if topk_out else None
         tp = torch.full((B, K), -1.0, dtype=torch.float32, device=dev) if topk_out else None
         fl = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -128,6 +128,13 @@ def compare(g, orc, cfg, check_topk=True, check_logits=True, label=""):
                 f"{label} row {r}: token {g['tokens'][r]} != oracle {tok} (path {tr.path}, "
                 f"boundary distance {d:.3e}, flags {g['flags'][r]:#x})")
             n_boundary += 1
+        if check_topk and tr.path == O.PATH_FULL and g["topk_prob"] is not None and g["tokens"][r] == tok:
+            # the full path reports the drawn token and its probability q / S
+            assert g["topk_idx"][r][0] == tok, f"{label} row {r}: full-path output index"
+            want = (tr.cdf_hi - tr.cdf_lo) / tr.sum_final if tr.sum_final > 0 and np.isfinite(tr.sum_final) else 0.0
+            gp = float(g["topk_prob"][r][0])
+            assert abs(gp - want) <= PROB_RTOL * abs(want) + 1e-30, \
+                f"{label} row {r}: full-path probability {gp} vs {want}"
         if check_topk and tr.path == O.PATH_TOPK and g["topk_idx"] is not None:
             idx, prob = canonical_topk(tr)
             K = tr.k

@@ -533,6 +533,8 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   const bool topk = path_any[kPathTopk], huge = path_any[kPathTopkHuge];
   if ((out->topk_idx || out->topk_prob) && (topk || huge) && out->topk_stride < (kmax > kmax_huge ? kmax : kmax_huge))
     return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= TopK");
+  if ((out->topk_idx || out->topk_prob) && path_any[kPathFull] && out->topk_stride < 1)
+    return fail(s, VDX_E_INVALID_ARG, "process_device: topk_stride must be >= 1");
   if (chunks_for(vocab) > kMaxChunks)
     return fail(s, VDX_E_UNSUPPORTED, "process_device: vocab > 4194304 is not supported");
   // TopK > 64 runs the large-K kernel, with more candidate slots per chunk
@@ -564,8 +566,8 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   p.rng.kind = s->rng_kind;
   p.rng.u_out = out->uniforms;
   p.out.tokens = out->tokens;
-  p.out.topk_idx = (topk || huge) ? out->topk_idx : nullptr;
-  p.out.topk_prob = (topk || huge) ? out->topk_prob : nullptr;
+  p.out.topk_idx = out->topk_idx;
+  p.out.topk_prob = out->topk_prob;
   p.out.topk_stride = out->topk_stride;
   p.out.flags = out->flags;
   p.meta = s->d_meta;
@@ -671,8 +673,8 @@ int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int3
   p.rng.kind = VDX_RNG_XOSHIRO;
   p.rng.u_out = out->uniforms;
   p.out.tokens = out->tokens;
-  p.out.topk_idx = path == 1 ? out->topk_idx : nullptr;
-  p.out.topk_prob = path == 1 ? out->topk_prob : nullptr;
+  p.out.topk_idx = path != kPathGreedy ? out->topk_idx : nullptr;
+  p.out.topk_prob = path != kPathGreedy ? out->topk_prob : nullptr;
   p.out.topk_stride = out->topk_stride;
   p.out.flags = out->flags;
   p.meta = reinterpret_cast<ChunkMeta *>(ws + kNaMeta);

@@ -2965,6 +2965,8 @@ struct FullSmem {
   int32_t cstar;
   int32_t whit[kWaves];
   int32_t wlast[kWaves];
+  float whitw[kWaves];   // the weight at whit / wlast
+  float wlastw[kWaves];
   double scale;
   double base;
   double cincl[kMaxChunks];
@@ -3136,6 +3138,9 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
     if (tid == 0) {
       p.out.tokens[row] = V - 1;
       if (p.out.flags) p.out.flags[row] = kRowFull | kRowNan | kRowFallback;
+      const int64_t o = (int64_t)row * p.out.topk_stride;
+      if (p.out.topk_idx) p.out.topk_idx[o] = V - 1;
+      if (p.out.topk_prob) p.out.topk_prob[o] = 0.0f;  // the weights are not finite
     }
     return;
   }
@@ -3242,43 +3247,68 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   const double tb = block_excl_scan_f64(tsum * scale, sm.wtot, segtot);
   double run = before + tb;
   int hit = -1, lastnz = -1;
+  float hitw = 0.0f, lastw = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const double w = (double)w16[i] * scale;
-    if (w16[i] > 0.0f) lastnz = e0 + i;
+    if (w16[i] > 0.0f) {
+      lastnz = e0 + i;
+      lastw = w16[i];
+    }
     run = run + w;
-    if (hit < 0 && w16[i] > 0.0f && run > t) hit = e0 + i;
+    if (hit < 0 && w16[i] > 0.0f && run > t) {
+      hit = e0 + i;
+      hitw = w16[i];
+    }
   }
   // thread order is index order here: the first hit is the lowest thread's,
   // the last non-zero weight the highest thread's (per wave by ballot; LDS
   // atomics with a different value per lane would run a scalar loop per wave)
   const uint64_t hb = __ballot(hit >= 0), nb = __ballot(lastnz >= 0);
-  const int hv = __shfl(hit, hb ? __ffsll((unsigned long long)hb) - 1 : 0);  // every lane active
-  const int nv = __shfl(lastnz, nb ? 63 - __clzll((long long)nb) : 0);
+  const int hl = hb ? __ffsll((unsigned long long)hb) - 1 : 0, nl = nb ? 63 - __clzll((long long)nb) : 0;
+  const int hv = __shfl(hit, hl);  // every lane active
+  const int nv = __shfl(lastnz, nl);
+  const float hw = __shfl(hitw, hl), nw = __shfl(lastw, nl);
   if (lane == 0) {
     sm.whit[wv] = hb ? hv : 0x7FFFFFFF;
     sm.wlast[wv] = nb ? nv : -1;
+    sm.whitw[wv] = hw;
+    sm.wlastw[wv] = nw;
   }
   __syncthreads();
   if (tid == 0) {
     int32_t tok;
     uint32_t fl2 = kRowFull;
     int32_t h = 0x7FFFFFFF, ln = -1;
+    float hw2 = 0.0f, lw2 = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      h = (h == 0x7FFFFFFF) ? sm.whit[w] : h;
-      ln = (sm.wlast[w] >= 0) ? sm.wlast[w] : ln;
+      if (h == 0x7FFFFFFF) {
+        h = sm.whit[w];
+        hw2 = sm.whitw[w];
+      }
+      if (sm.wlast[w] >= 0) {
+        ln = sm.wlast[w];
+        lw2 = sm.wlastw[w];
+      }
     }
-    if (h != 0x7FFFFFFF)
+    float wt = 0.0f;
+    if (h != 0x7FFFFFFF) {
       tok = h;
-    else if (ln >= 0)
+      wt = hw2;
+    } else if (ln >= 0) {
       tok = ln;
-    else {
+      wt = lw2;
+    } else {
       tok = V - 1;
       fl2 |= kRowFallback;
     }
     p.out.tokens[row] = tok;
     if (p.out.flags) p.out.flags[row] = fl2;
+    // entry 0 of the top-K outputs: the drawn token and its probability q / S
+    const int64_t o = (int64_t)row * p.out.topk_stride;
+    if (p.out.topk_idx) p.out.topk_idx[o] = tok;
+    if (p.out.topk_prob) p.out.topk_prob[o] = (total > 0.0) ? (float)((double)wt * scale / total) : 0.0f;
   }
 }
 
