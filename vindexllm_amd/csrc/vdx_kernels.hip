@@ -2950,26 +2950,25 @@ __device__ __forceinline__ float exp_nonpos(float x) {
 }
 
 struct FullSmem {
-  union {
-    PenaltySmem pen;          // stream phase: the fused penalty's table
-    float wseg[kWaveSpan];    // last workgroup: the target segment's weights
-  };
+  PenaltySmem pen;  // stream phase: the fused penalty's table
   float wm[kWaves];
   uint32_t wf[kWaves];
   double wd[kWaves];
   double wtot[kWaves];
   int32_t last;
-  float M;
-  uint32_t bad;
-  float u;
-  int32_t cstar;
+  int32_t cstar;  // finish: -1 when the row's weights are not finite
   int32_t whit[kWaves];
   int32_t wlast[kWaves];
-  float whitw[kWaves];   // the weight at whit / wlast
+  float whitw[kWaves];  // the weight at whit / wlast
   float wlastw[kWaves];
+  // the target segment, set by wave 0 for the rescan
+  int32_t seg0;
+  float tcm;
+  float M;
+  double before;
   double scale;
-  double base;
-  double cincl[kMaxChunks];
+  double total;
+  double tval;
 };
 
 template <bool VEC>
@@ -3082,16 +3081,25 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   }
   double acc = 0.0;
   if (base > -INFINITY && base < INFINITY) {
+    if (EXACT) {
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      float w;
-      if (EXACT) {
+      for (int i = 0; i < kPerThread; ++i) {
         const float q = (float)exp((double)v[i] - (double)base);
-        w = (q < p.min_p) ? 0.0f : q;
-      } else {
-        w = exp_nonpos(v[i] - base);
+        acc += (double)((q < p.min_p) ? 0.0f : q);
       }
-      acc += (double)w;
+    } else {
+      // a pairwise fp32 tree (no serial chain of fp64 adds): the sum of 64
+      // non-negative weights is within 6 * 2^-24 (relative) of the exact one,
+      // inside the single pass's draw tolerance; the target segment is
+      // rescanned in fp64 by the finish
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i) v[i] = exp_nonpos(v[i] - base);
+#pragma unroll
+      for (int h = kPerThread / 2; h >= 1; h >>= 1) {
+#pragma unroll
+        for (int i = 0; i < h; ++i) v[i] = v[i] + v[i + h];
+      }
+      acc = (double)v[0];
     }
   }
   const double ws = wave_sum_f64(acc);
@@ -3114,98 +3122,159 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
 
   // ---- finish (last workgroup of the row) ----
-  if (tid == 0) sm.u = rng_draw(p.rng, row, rp);
-  float mc = -INFINITY;
-  uint32_t fl = 0u;
-  double dc = 0.0;
-  if (tid < S) {
-    const uint64_t w0 = xload(&fm[tid].w[0]);
-    mc = __uint_as_float((uint32_t)w0);
-    fl = (uint32_t)(w0 >> 32);
-    dc = __longlong_as_double((long long)xload(&fm[tid].w[1]));
-  }
-  const float wmx = wave_max_f32(mc);
-  const uint32_t wfl = wave_or_u32(fl);
-  __syncthreads();
-  if (lane == 0) {
-    sm.wm[wv] = wmx;
-    sm.wf[wv] = wfl;
-  }
-  __syncthreads();
-  const float M = EXACT ? base : fmaxf(fmaxf(sm.wm[0], sm.wm[1]), fmaxf(sm.wm[2], sm.wm[3]));
-  const bool rowbad = (sm.wf[0] | sm.wf[1] | sm.wf[2] | sm.wf[3]) || !(M > -INFINITY && M < INFINITY);
-  if (rowbad) {
-    if (tid == 0) {
-      p.out.tokens[row] = V - 1;
-      if (p.out.flags) p.out.flags[row] = kRowFull | kRowNan | kRowFallback;
-      const int64_t o = (int64_t)row * p.out.topk_stride;
-      if (p.out.topk_idx) p.out.topk_idx[o] = V - 1;
-      if (p.out.topk_prob) p.out.topk_prob[o] = 0.0f;  // the weights are not finite
-    }
-    return;
-  }
-  // chunk weights and their running sum in chunk order
-  double wc = 0.0;
-  if (tid < S) wc = EXACT ? dc : dc * exp((double)mc - (double)M);
-  double total;
-  const double excl = block_excl_scan_f64(wc, sm.wtot, total);
-  const double incl = excl + wc;
-  if (tid < S) sm.cincl[tid] = incl;
-  if (tid == 0) {
-    sm.cstar = 0x7FFFFFFF;
-  }
-  __syncthreads();
-  const double t = (double)sm.u * total;
-  {
-    const uint64_t h = __ballot(tid < S && incl > t);
-    if (h && lane == __ffsll((unsigned long long)h) - 1) atomicMin(&sm.cstar, (int)tid);
-  }
-  __syncthreads();
-  int cs = (sm.cstar != 0x7FFFFFFF) ? sm.cstar : -1;  // first chunk whose running sum exceeds t
-  if (cs < 0) {
-    // rounding put t at or past the total: take the last chunk that weighs
-    for (int c = S - 1; c >= 0; --c)
-      if (sm.cincl[c] > (c ? sm.cincl[c - 1] : 0.0)) {
-        cs = c;
-        break;
+  // Wave 0 reads the chunk records and finds the row maximum M, the chunk
+  // weights exp(m_c - M) D_c and their running sums in chunk order, the
+  // target chunk (the first whose running sum exceeds t = u S) and, in it,
+  // the target 4096-logit segment; the workgroup meets at one barrier and
+  // rescans that segment.
+  if (wv == 0) {
+    float u = 0.0f;
+    if (lane == 0) u = rng_draw(p.rng, row, rp);
+    u = __shfl(u, 0);
+    // lane l holds chunks [l * per, l * per + per); each record comes in one
+    // round trip
+    constexpr int kPer = kMaxChunks / 64;
+    const int per = (S + 63) >> 6;
+    float mc[kPer];
+    double dc[kPer], cw[kPer][kWaves];
+    uint32_t fl = 0u;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int c = lane * per + k;
+      mc[k] = -INFINITY;
+      dc[k] = 0.0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) cw[k][w] = 0.0;
+      if (k < per && c < S) {
+        uint64_t r[2 + kWaves];
+#pragma unroll
+        for (int j = 0; j < 2 + kWaves; ++j) r[j] = xload(&fm[c].w[j]);
+        mc[k] = __uint_as_float((uint32_t)r[0]);
+        fl |= (uint32_t)(r[0] >> 32);
+        dc[k] = __longlong_as_double((long long)r[1]);
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) cw[k][w] = __longlong_as_double((long long)r[2 + w]);
+        mx = fmaxf(mx, mc[k]);
       }
-    if (cs < 0) cs = S - 1;
-  }
-  // segment of the target chunk (4096-logit wave spans), sequentially
-  const float tcm = __uint_as_float((uint32_t)xload(&fm[cs].w[0]));
-  double tdw[kWaves];
+    }
+    const float M = EXACT ? base : wave_max_f32(mx);
+    const bool rowbad = wave_or_u32(fl) != 0u || !(M > -INFINITY && M < INFINITY);
+    if (rowbad) {
+      if (lane == 0) {
+        p.out.tokens[row] = V - 1;
+        if (p.out.flags) p.out.flags[row] = kRowFull | kRowNan | kRowFallback;
+        const int64_t o = (int64_t)row * p.out.topk_stride;
+        if (p.out.topk_idx) p.out.topk_idx[o] = V - 1;
+        if (p.out.topk_prob) p.out.topk_prob[o] = 0.0f;  // the weights are not finite
+        sm.cstar = -1;
+      }
+    } else {
+      double wc[kPer], part[kPer], acc = 0.0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) tdw[w] = __longlong_as_double((long long)xload(&fm[cs].w[2 + w]));
-  const double scale = EXACT ? 1.0 : exp((double)tcm - (double)M);
-  double before = cs ? sm.cincl[cs - 1] : 0.0;
-  int ws_ = -1;
-  for (int w = 0; w < kWaves; ++w) {
-    const double ww = tdw[w] * scale;
-    if (before + ww > t) {
-      ws_ = w;
-      break;
+      for (int k = 0; k < kPer; ++k) {
+        wc[k] = 0.0;
+        if (k < per && lane * per + k < S) wc[k] = EXACT ? dc[k] : dc[k] * exp((double)mc[k] - (double)M);
+        acc = acc + wc[k];
+        part[k] = acc;
+      }
+      const double lincl = wave_incl_scan_f64(acc);
+      const double total = __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(lincl), 63));
+      const double t = (double)u * total;
+      // incl[k]: the running sum through chunk lane * per + k; prv[k]: through
+      // the chunk before it (for k = 0 the previous lane's last, 0 on lane 0)
+      const double lexcl = lincl - acc;
+      double incl[kPer], prv[kPer];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) incl[k] = lexcl + part[k];
+      double lastincl = incl[0];
+#pragma unroll
+      for (int k = 1; k < kPer; ++k)
+        if (k < per) lastincl = incl[k];
+      const double up = __longlong_as_double((long long)__shfl_up((long long)__double_as_longlong(lastincl), 1));
+      prv[0] = lane ? up : 0.0;
+#pragma unroll
+      for (int k = 1; k < kPer; ++k) prv[k] = incl[k - 1];
+      // the first chunk whose running sum exceeds t; if rounding put t at or
+      // past the total, the last chunk that weighs (its running sum grows)
+      int hk = -1, nk = -1;
+#pragma unroll
+      for (int k = kPer - 1; k >= 0; --k) {
+        const bool real = k < per && lane * per + k < S;
+        if (real && incl[k] > t) hk = k;
+        if (real && nk < 0 && incl[k] > prv[k]) nk = k;
+      }
+      const uint64_t hb = __ballot(hk >= 0), nb = __ballot(nk >= 0);
+      int sl, sk;
+      if (hb) {
+        sl = __ffsll((unsigned long long)hb) - 1;
+        sk = __shfl(hk, sl);
+      } else if (nb) {
+        sl = 63 - __clzll((long long)nb);
+        sk = __shfl(nk, sl);
+      } else {
+        sl = (S - 1) / per;
+        sk = (S - 1) - sl * per;
+      }
+      if (lane == sl) {
+        // the target chunk's record, selected without indexing the
+        // register arrays by a run-time value
+        float tcm = mc[0];
+        double tdw[kWaves], before = prv[0];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) tdw[w] = cw[0][w];
+#pragma unroll
+        for (int k = 1; k < kPer; ++k)
+          if (k == sk) {
+            tcm = mc[k];
+            before = prv[k];
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) tdw[w] = cw[k][w];
+          }
+        const double scale = EXACT ? 1.0 : exp((double)tcm - (double)M);
+        const double b0 = before;
+        int ws_ = -1;
+        for (int w = 0; w < kWaves; ++w) {
+          const double ww = tdw[w] * scale;
+          if (before + ww > t) {
+            ws_ = w;
+            break;
+          }
+          before = before + ww;
+        }
+        if (ws_ < 0) {
+          ws_ = kWaves - 1;
+          before = b0;
+          for (int w = 0; w < kWaves - 1; ++w) before = before + tdw[w] * scale;
+          while (ws_ > 0 && tdw[ws_] == 0.0) {
+            --ws_;
+            before = before - tdw[ws_] * scale;
+          }
+        }
+        sm.seg0 = (sl * per + sk) * kChunk + ws_ * kWaveSpan;
+        sm.before = before;
+        sm.scale = scale;
+        sm.total = total;
+        sm.tval = t;
+        sm.tcm = tcm;
+        sm.M = M;
+        sm.cstar = 0;
+      }
     }
-    before = before + ww;
   }
-  if (ws_ < 0) {
-    ws_ = kWaves - 1;
-    before = cs ? sm.cincl[cs - 1] : 0.0;
-    for (int w = 0; w < kWaves - 1; ++w) before = before + tdw[w] * scale;
-    while (ws_ > 0 && tdw[ws_] == 0.0) {
-      --ws_;
-      before = before - tdw[ws_] * scale;
-    }
-  }
-  // rescan that segment: its weights are computed from coalesced loads
-  // (consecutive lanes read consecutive float4s; penalised values written by
-  // the row's other workgroups are read past the caches) into LDS in index
-  // order, then thread tid takes 16 consecutive weights
-  const int seg0 = cs * kChunk + ws_ * kWaveSpan;
+  __syncthreads();
+  if (sm.cstar < 0) return;
+  // rescan the target segment: thread tid takes 16 consecutive logits (the
+  // wave's four loads cover its 4 KiB; penalised values written by the row's
+  // other workgroups are read past the caches)
+  const int seg0 = sm.seg0;
+  const double scale = sm.scale, total = sm.total, t = sm.tval;
+  const float tcm = sm.tcm, M = sm.M;
   const int e0 = seg0 + tid * 16;
+  float w16[16];
 #pragma unroll
-  for (int q = 0; q < kWaveSpan / (4 * kBlock); ++q) {
-    const int o = q * 4 * kBlock + tid * 4;
-    const int e = seg0 + o;
+  for (int q = 0; q < 4; ++q) {
+    const int e = e0 + 4 * q;
     float x[4];
     if (VEC && e < V) {  // 16-byte aligned rows, V % 4 = 0: the float4 lies in the row
       const f32x4 f = p.fuse_penalty ? xload4(&L[e]) : *reinterpret_cast<const f32x4 *>(&L[e]);
@@ -3218,7 +3287,6 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
       for (int i = 0; i < 4; ++i)
         x[i] = (e + i < V) ? (p.fuse_penalty ? xloadf(&L[e + i]) : L[e + i]) : 0.0f;
     }
-    f32x4 w4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float w = 0.0f;
@@ -3231,21 +3299,15 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
           w = exp_nonpos(s - tcm);
         }
       }
-      w4[i] = w;
+      w16[4 * q + i] = w;
     }
-    *reinterpret_cast<f32x4 *>(&sm.wseg[o]) = w4;
   }
-  __syncthreads();
-  float w16[16];
   double tsum = 0.0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    w16[i] = sm.wseg[tid * 16 + i];
-    tsum += (double)w16[i];
-  }
+  for (int i = 0; i < 16; ++i) tsum += (double)w16[i];
   double segtot;
   const double tb = block_excl_scan_f64(tsum * scale, sm.wtot, segtot);
-  double run = before + tb;
+  double run = sm.before + tb;
   int hit = -1, lastnz = -1;
   float hitw = 0.0f, lastw = 0.0f;
 #pragma unroll
