@@ -159,7 +159,10 @@ int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int3
  *   logits[r*logit_stride + v] = sum_e dequant(W[v][e]) * hidden[r*in_dim + e].
  * `weights`: vocab rows of in_dim/32 Q4_0 blocks (18 bytes: fp16 scale, then
  * 16 bytes of nibbles; GGUFReader.pas:264-281), 16-byte aligned; in_dim must
- * be a multiple of 256.  `scratch` holds an element-major copy of up to 16
+ * be a multiple of 32 (one block), as matvec_q4_0.comp takes it; rows whose
+ * length is not a multiple of 256 read their last blocks with 2-byte loads,
+ * and in the GGUF layout every block of such rows does (the packed layout
+ * keeps whole slices fast).  `scratch` holds an element-major copy of up to 16
  * hidden rows: at least 16*in_dim floats when rows > 1 (may be NULL when
  * rows == 1).  Every pointer is device memory.  Stream-ordered,
  * asynchronous, allocates nothing; the message of a failure is
@@ -184,7 +187,7 @@ int vdx_lmhead_q4_0(const void *weights, const float *hidden, int32_t rows, int3
  * skipped when `norm_weight` is NULL, then the lm_head in the weight tensor's
  * own format `wtype` (VDX_TENSOR_*), as TVdxAttention.DispatchMatVec issues it
  * (Attention.pas:979-1025): logits[r*logit_stride + v] = sum_e W(v,e) * xn_r[e].
- * `weights` is 16-byte aligned; in_dim is a multiple of 256; `scratch` (at
+ * `weights` is 16-byte aligned; in_dim is a multiple of 32; `scratch` (at
  * least 16*in_dim floats) holds the prepared hidden rows and is required when
  * rows > 1 or with the norm.  Every pointer is device memory.  Stream-ordered,
  * asynchronous, allocates nothing; a failure's message is

@@ -101,7 +101,7 @@ def test_lmhead_argument_errors_need_no_gpu():
     al = (base + 15) & ~15
     hid = C.c_void_p(al)
     cases = [
-        (C.c_void_p(al), hid, 1, 100, 1024, "multiple of 256"),   # in_dim
+        (C.c_void_p(al), hid, 1, 100, 1024, "multiple of 32"),    # in_dim
         (C.c_void_p(al + 4), hid, 1, 256, 1024, "aligned"),       # weights alignment
         (None, hid, 1, 256, 1024, "required"),                    # weights
         (C.c_void_p(al), hid, 0, 256, 1024, "rows > 0"),          # rows

@@ -233,7 +233,10 @@ def gpu_lmhead_any(w, wtype, H, V, norm=None, eps=1e-6):
 @pytest.mark.parametrize("wtype", [O.TENSOR_Q8_0, O.TENSOR_F16, O.TENSOR_Q4_0])
 @pytest.mark.parametrize("V,D,B,norm", [(4096 + 77, 256, 1, False), (4096 + 77, 256, 3, True),
                                         (2048, 512, 8, False), (1000, 2560, 16, True),
-                                        (1000, 2560, 1, True), (300, 256, 17, False)])
+                                        (1000, 2560, 1, True), (300, 256, 17, False),
+                                        # in_dim not a whole number of slices (Gemma-3-1B's 1152,
+                                        # 45 blocks, one block): the tail blocks
+                                        (1000, 1152, 1, False), (777, 1440, 3, True), (300, 32, 2, False)])
 def test_lmhead_formats_and_norm_bit_exact(wtype, V, D, B, norm):
     # every format's logits equal the oracle's restatement of the kernel's
     # summation order, on the output-RMSNorm'd rows when the norm is fused
@@ -333,7 +336,8 @@ def test_lmhead_from_gguf_file(tmp_path, wtype):
 
 def _pack_ref(w, wtype, D, V):
     """The packed layout restated with numpy: for each 64-row group, slice s
-    and piece k, the 64 rows' pieces in row order (rows past V are zero)."""
+    and piece k, the 64 rows' pieces in row order, then the rows' tail blocks
+    (D not a whole number of slices) row after row (rows past V are zero)."""
     bb = {O.TENSOR_Q4_0: 18, O.TENSOR_Q8_0: 34, O.TENSOR_F16: 64}[wtype]
     P, PB, SE = {O.TENSOR_Q4_0: (9, 16, 256), O.TENSOR_Q8_0: (17, 8, 128), O.TENSOR_F16: (8, 16, 64)}[wtype]
     rowbytes = D // 32 * bb
@@ -341,19 +345,23 @@ def _pack_ref(w, wtype, D, V):
     rows = np.zeros((nw * 64, rowbytes), dtype=np.uint8)
     rows[:V] = w.reshape(V, rowbytes)
     ns = D // SE
-    t = rows.reshape(nw, 64, ns, P, PB)            # wave, lane, slice, piece, bytes
-    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(-1)
+    mainb = ns * P * PB
+    groups = rows.reshape(nw, 64, rowbytes)
+    main = groups[:, :, :mainb].reshape(nw, 64, ns, P, PB).transpose(0, 2, 3, 1, 4).reshape(nw, -1)
+    tail = groups[:, :, mainb:].reshape(nw, -1)    # each group's rows, their tail bytes in row order
+    return np.ascontiguousarray(np.concatenate([main, tail], axis=1)).reshape(-1)
 
 
 @pytest.mark.parametrize("wtype", [O.TENSOR_Q4_0, O.TENSOR_Q8_0, O.TENSOR_F16])
-def test_lmhead_pack_layout(wtype):
+@pytest.mark.parametrize("D", [512, 1440])
+def test_lmhead_pack_layout(wtype, D):
     # the pack kernel's output equals the layout restated with numpy
     import torch
 
     from vindexllm_amd import lmhead_pack, lmhead_packed_bytes
 
-    V, D = 200, 512
-    log(f"[case] lm_head pack layout wtype={wtype}")
+    V = 200
+    log(f"[case] lm_head pack layout wtype={wtype} D={D}")
     rng = np.random.default_rng(9300 + wtype)
     w = {O.TENSOR_Q8_0: rand_q8_0, O.TENSOR_F16: rand_f16, O.TENSOR_Q4_0: rand_q4_0}[wtype](rng, V, D)
     p = lmhead_pack(torch.from_numpy(w).cuda(), wtype, D, V)
@@ -366,7 +374,8 @@ def test_lmhead_pack_layout(wtype):
 @pytest.mark.parametrize("wtype", [O.TENSOR_Q4_0, O.TENSOR_Q8_0, O.TENSOR_F16])
 @pytest.mark.parametrize("V,D,B,norm", [(4096 + 77, 256, 1, False), (4096 + 77, 768, 3, True),
                                         (2048, 512, 8, False), (1000, 2560, 16, True),
-                                        (300, 2560, 1, True), (63, 256, 17, False)])
+                                        (300, 2560, 1, True), (63, 256, 17, False),
+                                        (1000, 1152, 3, True), (300, 1440, 1, False), (129, 96, 16, False)])
 def test_lmhead_packed_matches_gguf_layout(wtype, V, D, B, norm):
     # the packed layout gives the same logits bit for bit (and so the oracle's)
     import torch

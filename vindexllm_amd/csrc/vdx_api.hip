@@ -795,7 +795,7 @@ static const char *lmhead_check(const void *weights, int32_t wtype, const float 
     *rc = VDX_E_UNSUPPORTED;
     return "lm_head: weight type must be VDX_TENSOR_Q4_0, VDX_TENSOR_Q8_0 or VDX_TENSOR_F16";
   }
-  if (in_dim <= 0 || in_dim % 256 != 0) return "lm_head: in_dim must be a positive multiple of 256";
+  if (in_dim <= 0 || in_dim % 32 != 0) return "lm_head: in_dim must be a positive multiple of 32";
   if ((uintptr_t)weights % 16 != 0) return "lm_head: weights must be 16-byte aligned";
   if ((int64_t)(in_dim / 32) * lm_block_bytes(wtype) * 64 > (int64_t)0x7FFFFFFF)
     return "lm_head: in_dim too large";
@@ -832,7 +832,7 @@ int vdx_lmhead(const void *weights, int32_t wtype, const float *hidden, const fl
 }
 
 int64_t vdx_lmhead_packed_bytes(int32_t wtype, int32_t in_dim, int32_t vocab) {
-  if (lm_block_bytes(wtype) == 0 || in_dim <= 0 || in_dim % 256 != 0 || vocab <= 0) return VDX_E_INVALID_ARG;
+  if (lm_block_bytes(wtype) == 0 || in_dim <= 0 || in_dim % 32 != 0 || vocab <= 0) return VDX_E_INVALID_ARG;
   return lmhead_packed_bytes(lm_format(wtype), in_dim, vocab);
 }
 
@@ -841,7 +841,7 @@ int vdx_lmhead_pack(const void *weights, int32_t wtype, int32_t in_dim, int32_t 
   const int64_t need = vdx_lmhead_packed_bytes(wtype, in_dim, vocab);
   if (need < 0 || !weights || !packed || packed_bytes < need || (uintptr_t)weights % 16 != 0 ||
       (uintptr_t)packed % 16 != 0 || (wtype & VDX_LMHEAD_PACKED)) {
-    g_call_err = "lm_head pack: need a VDX_TENSOR_* format, in_dim % 256 == 0, 16-byte aligned buffers "
+    g_call_err = "lm_head pack: need a VDX_TENSOR_* format, in_dim % 32 == 0, 16-byte aligned buffers "
                  "and packed_bytes >= vdx_lmhead_packed_bytes()";
     return VDX_E_INVALID_ARG;
   }

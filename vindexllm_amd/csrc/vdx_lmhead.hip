@@ -170,6 +170,35 @@ __device__ __forceinline__ void lm_slice(const uint32_t (&r)[slice_dw<FMT>()], c
   }
 }
 
+// One block of a row's tail (the blocks after its last whole slice, when
+// in_dim is not a multiple of the slice length), read from a 2-byte aligned
+// address (F16 blocks: 4-byte aligned); x points at the block's first hidden
+// value.  The arithmetic is the slices' (block_fma), so the block order of
+// the sum is unchanged.
+template <int FMT, int NB>
+__device__ __forceinline__ void lm_tail_block(const uint8_t *__restrict__ p, const float *__restrict__ x,
+                                              float (&acc)[NB]) {
+  if constexpr (FMT == kLmQ4_0) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    uint32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = (uint32_t)h[1 + 2 * j] | ((uint32_t)h[2 + 2 * j] << 16);
+    q4_block<NB>(q, (uint32_t)h[0], x, acc);
+  } else if constexpr (FMT == kLmQ8_0) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    uint32_t q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = (uint32_t)h[1 + 2 * j] | ((uint32_t)h[2 + 2 * j] << 16);
+    q8_block<NB>(q, (uint32_t)h[0], x, acc);
+  } else {
+    const uint32_t *d = reinterpret_cast<const uint32_t *>(p);
+    f16x2 w[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) w[k] = __builtin_bit_cast(f16x2, d[k]);
+    block_fma<NB>(w, 1.0f, x, acc);
+  }
+}
+
 template <int FMT> struct PieceT;
 template <> struct PieceT<kLmQ4_0> { typedef u32x4 T; };
 template <> struct PieceT<kLmQ8_0> { typedef u32x2 T; };
@@ -189,7 +218,14 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
   const int nrows = min(64, vocab - v0);
   // unsigned arithmetic: in_dim > 0 (the signed forms cost registers here)
   const int rowbytes = (int)(((uint32_t)in_dim >> 5) * (uint32_t)F::kBlockBytes);
-  const int nslices = (int)((uint32_t)in_dim / (uint32_t)SE);
+  // Whole slices, then the tail blocks.  In the GGUF layout a Q4_0 / Q8_0
+  // row whose length is not a whole number of slices does not start on a
+  // piece boundary, so there every block takes the tail path (2-byte loads).
+  const int nslices = (PACKED || FMT == kLmF16 || (uint32_t)in_dim % (uint32_t)SE == 0u)
+                          ? (int)((uint32_t)in_dim / (uint32_t)SE)
+                          : 0;
+  const int nmain = nslices * F::kNBlk;                    // blocks in whole slices
+  const int ntail = (int)((uint32_t)in_dim >> 5) - nmain;  // blocks after them
   float acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
@@ -199,7 +235,10 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
     // at ((s * P + k) * 64 + t) * PB from the wave's base, so each load
     // instruction reads 64 consecutive pieces and every cache line is fetched
     // once; the lane receives its own row's slice, with no transpose
-    const uint8_t *wp = wq + (int64_t)blockIdx.x * (int64_t)nslices * (P * 64 * PB) + t * PB;
+    // the group's 64 rows: whole slices as above, then each row's tail blocks
+    // row after row
+    const uint8_t *wg = wq + (int64_t)blockIdx.x * 64 * rowbytes;
+    const uint8_t *wp = wg + t * PB;
     Piece ca[P], cb[P];
     auto load = [&](Piece (&dst)[P], int sl) {
 #pragma unroll
@@ -214,7 +253,7 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
         for (int k = 0; k < PD; ++k) r[PD * j + k] = src[j][k];
       lm_slice<FMT, NB>(r, x + SE * NB * sl, acc);
     };
-    load(ca, 0);
+    if (nslices > 0) load(ca, 0);  // (a row shorter than one slice is all tail)
     for (int s = 0; s < nslices; s += 2) {
       if (s + 1 < nslices) load(cb, s + 1);
       compute(ca, s);
@@ -222,6 +261,12 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
         if (s + 2 < nslices) load(ca, s + 2);
         compute(cb, s + 1);
       }
+    }
+    if (ntail > 0) {  // fewer than kNBlk blocks: uniform branches, no loop-carried state
+      const uint8_t *tp = wg + (int64_t)nslices * (P * 64 * PB) + t * (ntail * F::kBlockBytes);
+#pragma unroll
+      for (int j = 0; j < F::kNBlk - 1; ++j)
+        if (j < ntail) lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc);
     }
     if (t < nrows) {
 #pragma unroll
@@ -250,7 +295,7 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
     for (int i = 0; i < P; ++i)
       pre[i] = __builtin_nontemporal_load(reinterpret_cast<const Piece *>(wt + goff[i] + P * PB * s));
   };
-  load_slice(0);
+  if (nslices > 0) load_slice(0);  // (no whole slice: every block is a tail block)
 
   for (int s = 0; s < nslices; ++s) {
     __syncthreads();  // the previous slice has been read (one wave: no-op ordering)
@@ -266,6 +311,11 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
       for (int k = 0; k < PD; ++k) r[PD * j + k] = v[k];
     }
     lm_slice<FMT, NB>(r, x + SE * NB * s, acc);
+  }
+  if (ntail > 0 && t < nrows) {  // rows past the vocabulary read nothing here
+    const uint8_t *tp = wt + (int64_t)t * rowbytes + nmain * F::kBlockBytes;
+    for (int j = 0; j < ntail; ++j)
+      lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc);
   }
   if (t < nrows) {
 #pragma unroll
@@ -313,30 +363,46 @@ __global__ __launch_bounds__(256) void k_lmhead_prep(const float *__restrict__ h
 
 // The packed layout of a weight tensor (vocab rows of in_dim elements in
 // format FMT): for each group of 64 rows (the last padded with zero rows),
-// each slice s and each piece k, the 64 rows' pieces in row order.  One
-// thread per destination piece; rows past the vocabulary are zero.
+// each whole slice s and each piece k, the 64 rows' pieces in row order; then
+// the rows' tail blocks (in_dim not a multiple of the slice length), row
+// after row.  One thread per destination piece; rows past the vocabulary are
+// zero.
 template <int FMT>
 __global__ __launch_bounds__(256) void k_lmhead_pack(const uint8_t *__restrict__ wq, uint8_t *__restrict__ out,
                                                       int32_t in_dim, int32_t vocab, int64_t npieces) {
   typedef LmFmt<FMT> F;
   typedef typename PieceT<FMT>::T Piece;
-  constexpr int P = F::kPieces, PB = 4 * F::kPieceDw, SE = 32 * F::kNBlk;
+  constexpr int P = F::kPieces, PB = 4 * F::kPieceDw, SE = 32 * F::kNBlk, BB = F::kBlockBytes;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= npieces) return;
   const int64_t nslices = in_dim / SE;
-  const int t = (int)(i & 63);
-  const int64_t q = i >> 6;  // (wave * nslices + s) * P + k
-  const int k = (int)(q % P);
-  const int64_t ws = q / P;
-  const int64_t s = ws % nslices, w = ws / nslices;
-  const int64_t row = w * 64 + t;
-  const int64_t rowbytes = (int64_t)(in_dim / 32) * F::kBlockBytes;
-  Piece v;
-  if (row < vocab)
-    v = *reinterpret_cast<const Piece *>(wq + row * rowbytes + (s * P + k) * PB);
-  else
-    v = Piece{};
-  *reinterpret_cast<Piece *>(out + i * PB) = v;
+  const int64_t nblocks = in_dim / 32, ntail = nblocks - nslices * F::kNBlk;
+  const int64_t rowbytes = nblocks * BB;
+  const int64_t per_group = 64 * rowbytes / PB;  // pieces per group of 64 rows
+  const int64_t w = i / per_group, ig = i - w * per_group;
+  const int64_t nmainp = nslices * P * 64;
+  if (ig < nmainp) {
+    const int t = (int)(ig & 63);
+    const int64_t q = ig >> 6;  // s * P + k
+    const int k = (int)(q % P);
+    const int64_t s = q / P;
+    const int64_t row = w * 64 + t;
+    Piece v;
+    if (row < vocab)
+      v = *reinterpret_cast<const Piece *>(wq + row * rowbytes + (s * P + k) * PB);
+    else
+      v = Piece{};
+    *reinterpret_cast<Piece *>(out + i * PB) = v;
+    return;
+  }
+  // tail region: row t's ntail blocks at t * ntail * BB; a piece may span two rows
+  const int64_t tbytes = ntail * BB;
+  const int64_t o0 = (ig - nmainp) * PB;
+  for (int b = 0; b < PB; ++b) {
+    const int64_t o = o0 + b;
+    const int64_t row = w * 64 + o / tbytes;
+    out[i * PB + b] = (row < vocab) ? wq[row * rowbytes + nslices * F::kNBlk * BB + o % tbytes] : (uint8_t)0;
+  }
 }
 
 int64_t lmhead_packed_bytes(int format, int in_dim, int vocab) {

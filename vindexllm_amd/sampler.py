@@ -472,7 +472,7 @@ def lmhead(weights, wtype: int, hidden, vocab: int, norm_weight=None, norm_eps: 
 def lmhead_packed_bytes(wtype: int, in_dim: int, vocab: int) -> int:
     n = load_library().vdx_lmhead_packed_bytes(int(wtype), int(in_dim), int(vocab))
     if n < 0:
-        raise VdxSamplerError(int(n), "lm_head pack: need a VDX_TENSOR_* format and in_dim % 256 == 0")
+        raise VdxSamplerError(int(n), "lm_head pack: need a VDX_TENSOR_* format and in_dim % 32 == 0")
     return int(n)
 
 
