@@ -91,7 +91,7 @@ WORKLOADS = {
              "top-k 40/min-p 0.05, full softmax; all penalised"),
 }
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
-                   "topk128_b64": "k_topk_big_vec", "topk_only_b64": "k_topk_vec",
+                   "topk128_b64": "k_topk_big_stream_vec", "topk_only_b64": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec", "mixed_rows_b64": "k_topk_vec"}
 

@@ -2530,9 +2530,15 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
   }
 }
 
+// Large K runs in two launches: the stream phase over every (row, chunk)
+// within the K <= 64 kernel's register and LDS budget (four workgroups per CU,
+// every chunk of a 64-row batch resident at once), then one workgroup per row
+// for the merge, the finish and the exact path, whose registers would
+// otherwise halve the stream phase's occupancy.  The launch boundary orders
+// the chunk records before the merge, so no ticket is taken.
 template <bool VEC>
-__device__ __forceinline__ void topk_body_big(const CallParams &p0) {
-  __shared__ TopkBigSmem sm;
+__device__ __forceinline__ void topk_big_stream_body(const CallParams &p0) {
+  __shared__ TopkSmem sm;
   int row, chunk;
   block_row_chunk(p0.nchunks, p0.rows, row, chunk);
   if (!row_on_path(p0, row, kPathTopk)) return;
@@ -2543,7 +2549,6 @@ __device__ __forceinline__ void topk_body_big(const CallParams &p0) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * ccap;
-  RngPre rp = rng_prefetch(p.rng, row);
   PenaltyPrefetch pf;
   if (p.fuse_penalty) {
     penalty_prefetch(p, row, pf);
@@ -2551,7 +2556,19 @@ __device__ __forceinline__ void topk_body_big(const CallParams &p0) {
   }
   topk_stream<VEC>(p, row, L, c0, clen, big_chunk_quota(K, S), cr + (int64_t)chunk * ccap, cm + chunk, pf, sm,
                    ccap);
-  if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void topk_big_finish_body(const CallParams &p0) {
+  __shared__ TopkBigSmem sm;
+  const int row = blockIdx.x;
+  if (!row_on_path(p0, row, kPathTopk)) return;
+  const CallParams p = for_row(p0, row);
+  const int S = p.nchunks, ccap = p.cand_cap;
+  const float *L = p.logits + (int64_t)row * p.stride;
+  const ChunkMeta *cm = p.meta + (int64_t)row * S;
+  const Cand *cr = p.cand + (int64_t)row * S * ccap;
+  RngPre rp = rng_prefetch(p.rng, row);
   if (threadIdx.x == 0) {
     sm.uval = rng_draw(p.rng, row, rp);
     sm.replay = 1;
@@ -2566,8 +2583,10 @@ __device__ __forceinline__ void topk_body_big(const CallParams &p0) {
   }
 }
 
-__global__ __launch_bounds__(kBlock) void k_topk_big_vec(CallParams p) { topk_body_big<true>(p); }
-__global__ __launch_bounds__(kBlock) void k_topk_big_scalar(CallParams p) { topk_body_big<false>(p); }
+__global__ __launch_bounds__(kBlock, 4) void k_topk_big_stream_vec(CallParams p) { topk_big_stream_body<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_big_stream_scalar(CallParams p) { topk_big_stream_body<false>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_big_finish_vec(CallParams p) { topk_big_finish_body<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_big_finish_scalar(CallParams p) { topk_big_finish_body<false>(p); }
 
 // =============================================================================
 // Top-K for K > kKBig (Sampler.pas:327-460): one workgroup per row replays
@@ -3490,11 +3509,14 @@ hipError_t launch_greedy(const CallParams &p, hipStream_t st) {
 }
 
 hipError_t launch_topk(const CallParams &p, hipStream_t st) {
-  if (p.cand_cap > kCandCap) {  // some row has 64 < K <= kKBig
-    if (p.vec)
-      hipLaunchKernelGGL(k_topk_big_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
-    else
-      hipLaunchKernelGGL(k_topk_big_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+  if (p.cand_cap > kCandCap) {  // some row has 64 < K <= kKBig: stream phase, then one workgroup per row
+    if (p.vec) {
+      hipLaunchKernelGGL(k_topk_big_stream_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+      hipLaunchKernelGGL(k_topk_big_finish_vec, dim3(p.rows), dim3(kBlock), 0, st, p);
+    } else {
+      hipLaunchKernelGGL(k_topk_big_stream_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+      hipLaunchKernelGGL(k_topk_big_finish_scalar, dim3(p.rows), dim3(kBlock), 0, st, p);
+    }
   } else if (p.vec) {
     hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
   } else {
