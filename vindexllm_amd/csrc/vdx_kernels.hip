@@ -280,6 +280,7 @@ struct TopkSmem {
   uint32_t xw[kWaves];   // exact path: candidates per wave in the current group
   uint32_t xmkey;        // exact path: key of the buffer's minimum
   int32_t xfrozen;       // exact path: L[0] is NaN, nothing enters
+  int32_t xdone;         // exact path: the slot-order finish ran in wave 0
   int32_t qnan;
   float wfmax[kWaves];
   double S;
@@ -1543,6 +1544,8 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   MinBuf mb{~0ull, 0xFFFFFFFFu, 0u};
   uint64_t *list = sm.buf.sk;  // one group's candidates in index order: ord_key << 32 | index
   float v[kPerThread];
+  uint64_t pk0 = 0ull, pk1 = 0ull;  // wave 0: the next chunk's candidate slots, loaded ahead
+  int pc = -1;                      // the chunk they belong to
   for (int c = 0; c < S; ++c) {
     const int c0 = c * kChunk, clen = min(kChunk, V - c0);
     __syncthreads();  // sm.ctau / the previous chunk's list and sm.xmkey
@@ -1556,11 +1559,25 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
         const uint32_t cap = (uint32_t)wave_cap(clen);
         const int sh = cap == 128u ? 7 : (cap == 64u ? 6 : 5);
         const uint32_t cnt = sm.ccount[c];
+        uint64_t raw[2];
+        if (pc == c) {
+          raw[0] = pk0;
+          raw[1] = pk1;
+        } else {
+          raw[0] = xload(&cc[2 * lane]);
+          raw[1] = xload(&cc[2 * lane + 1]);
+        }
+        if (c + 1 < S) {  // the next chunk's slots, in flight while this one is fed
+          const Cand *cn = cand_row + (int64_t)(c + 1) * kCandCap;
+          pk0 = xload(&cn[2 * lane]);
+          pk1 = xload(&cn[2 * lane + 1]);
+          pc = c + 1;
+        }
         uint64_t x[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const uint32_t slot = 2u * (uint32_t)lane + (uint32_t)e;
-          const uint64_t k = xload(&cc[slot]);
+          const uint64_t k = raw[e];
           const bool ok = (slot & (cap - 1u)) < ((cnt >> (8 * (slot >> sh))) & 0xFFu) &&
                           (uint32_t)(k >> 32) > mk;
           // sorted by index: index << 32 | key
@@ -1675,11 +1692,42 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
       sm.q[lane] = q;
     }
     const uint64_t nanm = __ballot(lane < K && q != q);
-    if (lane == 0) sm.qnan = nanm != 0ull;
+    if (lane == 0) {
+      sm.qnan = nanm != 0ull;
+      sm.xdone = 0;
+    }
+    // Top-P >= 1 (the draw walks the slots) with finite weights: when every
+    // non-zero q is within 2^22 of the largest, every fp64 partial sum of
+    // the <= 64 q is exact in any order, so wave scans give the slot-order
+    // sums of :386-410 and :447-459 bit for bit (else lane 0 below)
+    if (!(p.top_p < 1.0f) && nanm == 0ull) {
+      const float qmax = wave_max_f32(lane < K ? q : 0.0f);
+      if (p.min_p > 0.0f && lane < K && q < qmax * p.min_p) q = 0.0f;  // Min-P: Qmax = the largest q
+      const float qfloor = ldexpf(qmax, -22);
+      if (__ballot(lane < K && !(q == 0.0f || q >= qfloor)) == 0ull) {
+        const double incl = wave_incl_scan_f64(lane < K ? (double)q : 0.0);
+        const double S = __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(incl), 63));
+        const double t = (double)sm.uval * S;
+        const uint64_t hit = __ballot(lane < K && incl > t);
+        const int pos = hit ? (__ffsll((unsigned long long)hit) - 1) : K - 1;
+        if (lane < K) {
+          sm.q_ord[lane] = q;
+          sm.i_ord[lane] = sm.slot_i[lane];
+          sm.v_ord[lane] = sm.slot_v[lane];
+        }
+        if (lane == 0) {
+          sm.token = sm.slot_i[pos];
+          sm.rowflags = kRowTopkReplay | (hit ? 0u : kRowFallback);
+          sm.S = S;
+          sm.xdone = 1;
+        }
+      }
+    }
   }
   __syncthreads();
+  const bool xdone = sm.xdone != 0;
   // sums and Min-P in slot order (:386-410)
-  if (tid == 0) {
+  if (tid == 0 && !xdone) {
     double S = 0.0;
     for (int k = 0; k < K; ++k) S = S + (double)sm.q[k];
     if (p.min_p > 0.0f) {
@@ -1699,7 +1747,8 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   }
   __syncthreads();
   // draw order: stable descending sort when Top-P runs (:412-429)
-  if (p.top_p < 1.0f) {
+  if (xdone) {
+  } else if (p.top_p < 1.0f) {
     if (!sm.qnan) {
       if (wv == 0 && lane < K) {
         const float qk = sm.q[lane];
@@ -1741,7 +1790,7 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   }
   __syncthreads();
   // Top-P cut (:431-444) and draw (:447-459)
-  if (tid == 0) {
+  if (tid == 0 && !xdone) {
     double S = sm.S;
     if (p.top_p < 1.0f) {
       const double target = (double)p.top_p * S;
