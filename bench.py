@@ -365,6 +365,7 @@ def parity_check(name, L, hist, seed=4242):
 
 
 LMHEAD_V, LMHEAD_D = 262144, 2560  # Gemma-3-4B tied lm_head (token_embd.weight)
+LMHEAD_CHAIN = 16  # calls per captured graph for the steady-state figures
 VALU_FP32_PEAK_TFLOPS = 157.3      # MI355X published FP32 vector peak (packed FMA)
 
 
@@ -448,6 +449,23 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True, eager=Fals
         torch.cuda.synchronize()
         res[tag] = dict(wall_us=1e6 * (time.perf_counter() - t0) / steps,
                         event_us=1e3 * e0.elapsed_time(e1) / steps)
+        if not eager:
+            # the same call CHAIN times over in one graph: the steady-state
+            # cost of a call inside a larger captured step (a decode loop's
+            # whole forward is one graph), without one graph launch per call
+            chain = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(chain, stream=cs):
+                for _ in range(LMHEAD_CHAIN):
+                    fn()
+            chain.replay()
+            torch.cuda.synchronize()
+            reps = max(1, steps // LMHEAD_CHAIN)
+            e0.record(rs)
+            for _ in range(reps):
+                chain.replay()
+            e1.record(rs)
+            torch.cuda.synchronize()
+            res[tag]["chain_event_us"] = 1e3 * e0.elapsed_time(e1) / (reps * LMHEAD_CHAIN)
     s.Free()
     head_us = res["lmhead"]["event_us"]
     weight_bytes = V * nb * bb
@@ -456,7 +474,9 @@ def run_lmhead(B, steps, warmup, fmt="q4_0", norm=False, packed=True, eager=Fals
     out = {"rows_per_s": B / (res["call"]["wall_us"] * 1e-6),
            "us_per_step": res["call"]["wall_us"],
            "call_event_us": res["call"]["event_us"],
+           "call_chain_event_us": res["call"].get("chain_event_us"),
            "lmhead_kernel_us": head_us,
+           "lmhead_chain_event_us": res["lmhead"].get("chain_event_us"),
            "lmhead_gbs": alg_bytes / (head_us * 1e-6) / 1e9,
            "lmhead_hbm_frac": alg_bytes / (head_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
            "lmhead_tflops": flops / (head_us * 1e-6) / 1e12,

@@ -580,11 +580,15 @@ void vdxo_matvec_q4_0(const uint8_t *w, const float *x, int32_t in_dim,
 }
 
 /* The same matvec in the accumulation order of the library's fused lm_head
- * kernel (not the shader's): per row, blocks k = 0.. in order, s = 0,
- * s = fmaf(q_i - 8, x[32k+i], s) for i = 0..31 (element order: low nibbles
- * of qs[0..15], then high nibbles), acc = fmaf(d_k, s, acc).  Mathematically
- * the same sum as matvec_q4_0.comp:57-83; only the fp32 rounding points
- * differ (the shader's own are unpinned under GLSL contraction). */
+ * kernel (not the shader's): per row, blocks k = 0.. in order, t = 0,
+ * t = fmaf(16 (q_i - 8), x[32k+i], t) for i = 0..31 (element order: low
+ * nibbles of qs[0..15], then high nibbles), acc = fmaf(d_k / 16, t, acc).
+ * The power-of-two scaling is exact, so this is the plain chain
+ * s = fmaf(q_i - 8, x, s), acc = fmaf(d_k, s, acc) wherever no partial sum is
+ * subnormal; the kernel computes the scaled form, restated here as computed.
+ * Mathematically the same sum as matvec_q4_0.comp:57-83; only the fp32
+ * rounding points differ (the shader's own are unpinned under GLSL
+ * contraction). */
 void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
                               int32_t rows, float *logits) {
   const int32_t bpr = in_dim >> 5;
@@ -594,13 +598,13 @@ void vdxo_matvec_q4_0_blocked(const uint8_t *w, const float *x, int32_t in_dim,
     for (int32_t k = 0; k < bpr; ++k) {
       const uint8_t *b = row + (int64_t)k * 18;
       const float d = vdxo_half_to_float((uint16_t)(b[0] | (b[1] << 8)));
-      float s = 0.0f;
+      float t = 0.0f;
       for (int32_t i = 0; i < 32; ++i) {
         const uint32_t raw = b[2 + (i & 15)];
         const int32_t q = (int32_t)((raw >> ((i >> 4) * 4)) & 0xFu) - 8;
-        s = fmaf((float)q, x[32 * k + i], s);
+        t = fmaf((float)(16 * q), x[32 * k + i], t);
       }
-      acc = fmaf(d, s, acc);
+      acc = fmaf(d * 0.0625f, t, acc);
     }
     logits[r] = acc;
   }

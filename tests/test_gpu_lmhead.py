@@ -97,6 +97,38 @@ def test_lmhead_special_values():
         assert np.array_equal(G[b], O.matvec_q4_0_blocked(w, H[b], D, V))
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_lmhead_subnormal_partial_sums(packed):
+    # hidden values at and below fp32's smallest normal: the partial sums are
+    # subnormal, where the kernel's scaled high-nibble chain (16 s, weights
+    # 16 (q - 8)) rounds differently from an unscaled one; the oracle restates
+    # the scaled form, so the logits stay bit-exact
+    import torch
+
+    from vindexllm_amd import VDX_LMHEAD_PACKED, lmhead, lmhead_pack
+
+    log(f"[case] lm_head subnormal partial sums packed={packed}")
+    V, D = 700, 1280
+    rng = np.random.default_rng(7100 + packed)
+    w = rand_q4_0(rng, V, D)
+    H = np.stack([rng.standard_normal(D) * 1e-40,
+                  np.where(np.arange(D) % 2 == 0, 1e-37, 1e-41) * rng.standard_normal(D),
+                  rng.standard_normal(D)]).astype(np.float32)
+    assert (np.abs(H[0]) < np.finfo(np.float32).tiny).all()
+    dev = torch.device("cuda:0")
+    wd, hd = torch.from_numpy(w).to(dev), torch.from_numpy(H).to(dev)
+    wt = O.TENSOR_Q4_0
+    if packed:
+        wd = lmhead_pack(wd, wt, D, V)
+        wt |= VDX_LMHEAD_PACKED
+    G = lmhead(wd, wt, hd, V).cpu().numpy()
+    for r in range(H.shape[0]):
+        want = O.matvec_q4_0_blocked(w, H[r], D, V)
+        assert np.array_equal(G[r].view(np.uint32), want.view(np.uint32)), \
+            f"row {r}: {np.flatnonzero(G[r].view(np.uint32) != want.view(np.uint32))[:5]}"
+    log(f"[done] lm_head subnormal partial sums packed={packed}")
+
+
 def _cfg5(B, seed):
     rng = np.random.default_rng(seed)
     V, D = 262144, 2560

@@ -20,8 +20,12 @@
 // row) and per block k of 32 elements in order, s = 0; s = fma(w_i, x[32k + i],
 // s) for i = 0..31 with w_i = q_i - 8 (Q4_0), q_i (Q8_0) or the fp16 value
 // (F16), each product exact before its single rounding; then acc = fma(d_k, s,
-// acc) (d_k = 1 for F16).  The shaders' own summation orders (256 or 64
-// strided lanes, then a tree) differ only at fp32 rounding level.
+// acc) (d_k = 1 for F16).  For Q4_0 the chain runs on t = 16 s, with weights
+// 16 (q_i - 8), and acc = fma(d_k / 16, t, acc): scaling by a power of two
+// commutes with every rounding, so this is the same sum bit for bit wherever
+// no partial sum is subnormal (or above 2^124); the oracle restates the
+// scaled form, so it agrees everywhere.  The shaders' own summation orders
+// (256 or 64 strided lanes, then a tree) differ only at fp32 rounding level.
 //
 // Output RMSNorm (optional, before the product), in the shader's order:
 // thread t of 256 sums h[e]^2 for e = t, t + 256, ... (product then sum),
@@ -39,9 +43,13 @@
 // enter the FMAs as SGPR operands; with more than one batch row (or the norm)
 // they are read from a prepared copy, element-major with 16 batch rows per
 // 64-byte line, so one scalar load feeds the independent accumulation chains
-// of an element.  Quantised weights become f16 pairs exactly (v_perm_b32 puts
-// each byte under a 0x64 byte, f16 1024 + u, and one packed f16 subtract
-// removes the offset) that v_fma_mix_f32 consumes directly.
+// of an element.  Quantised weights become f16 pairs exactly, which
+// v_fma_mix_f32 consumes directly: a Q4_0 nibble pair is one v_and_or_b32
+// (the nibbles of bytes 0 and 2 of a dword, or of bytes 1 and 3 after one
+// shift, under a 0x64 byte: f16 1024 + q, or 1024 + 16 q for the high
+// nibbles, left in place) and one packed f16 fma or subtract to 16 (q - 8); a
+// Q8_0 byte pair is one v_perm_b32 (each byte under a 0x64 byte) and one
+// packed subtract.
 #include "vdx_internal.hpp"
 
 namespace vdx {
@@ -94,21 +102,55 @@ __device__ __forceinline__ float half_bits(uint32_t bits) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
 }
 
-// Q4_0 block: qs dwords q[0..3], scale bits dbits.
+// The Q4_0 nibble masks and the f16 exponent byte pair, in VGPRs: gfx950's
+// VOP3 encoding takes no literal, and with all three in registers each
+// (u & mask) | 0x64006400 is one v_and_or_b32 (with literals the compiler
+// emits an AND and an OR).
+struct Q4K {
+  uint32_t lo, hi, c;
+};
+__device__ __forceinline__ Q4K q4_consts() {
+  Q4K k;
+  asm("v_mov_b32 %0, 0x000F000F" : "=v"(k.lo));
+  asm("v_mov_b32 %0, 0x00F000F0" : "=v"(k.hi));
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(k.c));
+  return k;
+}
+
+// Q4_0 block: qs dwords q[0..3] (byte b of dword j is qs[4j + b]: low nibble
+// element 4j + b, high nibble element 16 + 4j + b), scale bits dbits.  Every
+// weight enters as 16 (q - 8): a low-nibble pair as 16 (1024 + q) - 16512 (one
+// packed f16 fma), a high-nibble pair, left in place, as 1024 + 16 q - 1152
+// (one packed f16 subtract), all exact; so the chain runs on t = 16 s and the
+// scale enters as d / 16 (exact for an fp16 d).
 template <int NB>
 __device__ __forceinline__ void q4_block(const uint32_t (&q)[4], uint32_t dbits, const float *__restrict__ x,
-                                         float (&acc)[NB]) {
+                                         float (&acc)[NB], const Q4K &K) {
+  const f16x2 m16 = {(_Float16)16, (_Float16)16}, o16 = {(_Float16)-16512, (_Float16)-16512};
+  const f16x2 o8 = {(_Float16)1152, (_Float16)1152};
+  // w[2j], w[2j + 1]: bytes 0 and 2, 1 and 3 (after the shift) of dword j;
+  // low nibbles in w[0..7], high nibbles in w[8..15]
   f16x2 w[16];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {  // offset 1024 + 8
-    const uint32_t lo = q[j] & 0x0F0F0F0Fu;
-    const uint32_t hi = (q[j] >> 4) & 0x0F0F0F0Fu;
-    w[2 * j] = byte_pair<1032>(lo, 0x04010400u);      // elements 4j, 4j+1
-    w[2 * j + 1] = byte_pair<1032>(lo, 0x04030402u);  // elements 4j+2, 4j+3
-    w[8 + 2 * j] = byte_pair<1032>(hi, 0x04010400u);  // elements 16+4j, 16+4j+1
-    w[9 + 2 * j] = byte_pair<1032>(hi, 0x04030402u);  // elements 16+4j+2, 16+4j+3
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t u = q[j], u8 = q[j] >> 8;
+    w[2 * j] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (u & K.lo) | K.c), m16, o16);
+    w[2 * j + 1] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (u8 & K.lo) | K.c), m16, o16);
+    w[8 + 2 * j] = __builtin_bit_cast(f16x2, (u & K.hi) | K.c) - o8;
+    w[9 + 2 * j] = __builtin_bit_cast(f16x2, (u8 & K.hi) | K.c) - o8;
   }
-  block_fma<NB>(w, half_bits(dbits), x, acc);
+  float t[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) t[b] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {  // element e = 16 h + 4 j + k: pair 8 h + 2 j + (k & 1), half k >> 1
+    const float we = (float)w[8 * (e >> 4) + 2 * ((e >> 2) & 3) + (e & 1)][(e >> 1) & 1];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) t[b] = __builtin_fmaf(we, x[e * NB + b], t[b]);
+  }
+  const float d16 = half_bits(dbits) * 0.0625f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = __builtin_fmaf(d16, t[b], acc[b]);
 }
 
 // Q8_0 block: qs dwords q[0..7] (four int8 each), scale bits dbits.
@@ -128,7 +170,7 @@ __device__ __forceinline__ void q8_block(const uint32_t (&q)[8], uint32_t dbits,
 // One slice of a row (dwords r[]), element-major hidden values x.
 template <int FMT, int NB>
 __device__ __forceinline__ void lm_slice(const uint32_t (&r)[slice_dw<FMT>()], const float *__restrict__ x,
-                                         float (&acc)[NB]) {
+                                         float (&acc)[NB], const Q4K &K) {
   if constexpr (FMT == kLmQ4_0) {
     // 4 block pairs of 9 dwords: the even block's scale in bytes 0-1 and qs in
     // bytes 2-17 (straddling dwords), the odd block's scale in bytes 18-19 and
@@ -140,9 +182,9 @@ __device__ __forceinline__ void lm_slice(const uint32_t (&r)[slice_dw<FMT>()], c
                               __builtin_amdgcn_alignbyte(pr[2], pr[1], 2),
                               __builtin_amdgcn_alignbyte(pr[3], pr[2], 2),
                               __builtin_amdgcn_alignbyte(pr[4], pr[3], 2)};
-      q4_block<NB>(qa, pr[0], x + 64 * m * NB, acc);
+      q4_block<NB>(qa, pr[0], x + 64 * m * NB, acc, K);
       const uint32_t qb[4] = {pr[5], pr[6], pr[7], pr[8]};
-      q4_block<NB>(qb, pr[4] >> 16, x + (64 * m + 32) * NB, acc);
+      q4_block<NB>(qb, pr[4] >> 16, x + (64 * m + 32) * NB, acc, K);
     }
   } else if constexpr (FMT == kLmQ8_0) {
     // 2 block pairs of 17 dwords: the even block's scale in bytes 0-1 and qs
@@ -177,13 +219,13 @@ __device__ __forceinline__ void lm_slice(const uint32_t (&r)[slice_dw<FMT>()], c
 // the sum is unchanged.
 template <int FMT, int NB>
 __device__ __forceinline__ void lm_tail_block(const uint8_t *__restrict__ p, const float *__restrict__ x,
-                                              float (&acc)[NB]) {
+                                              float (&acc)[NB], const Q4K &K) {
   if constexpr (FMT == kLmQ4_0) {
     const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
     uint32_t q[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = (uint32_t)h[1 + 2 * j] | ((uint32_t)h[2 + 2 * j] << 16);
-    q4_block<NB>(q, (uint32_t)h[0], x, acc);
+    q4_block<NB>(q, (uint32_t)h[0], x, acc, K);
   } else if constexpr (FMT == kLmQ8_0) {
     const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
     uint32_t q[8];
@@ -229,6 +271,8 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
   float acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+  Q4K K{};
+  if constexpr (FMT == kLmQ4_0) K = q4_consts();
 
   if constexpr (PACKED) {
     // packed layout (k_lmhead_pack): piece k of slice s of the wave's row t
@@ -251,7 +295,7 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
       for (int j = 0; j < P; ++j)
 #pragma unroll
         for (int k = 0; k < PD; ++k) r[PD * j + k] = src[j][k];
-      lm_slice<FMT, NB>(r, x + SE * NB * sl, acc);
+      lm_slice<FMT, NB>(r, x + SE * NB * sl, acc, K);
     };
     if (nslices > 0) load(ca, 0);  // (a row shorter than one slice is all tail)
     for (int s = 0; s < nslices; s += 2) {
@@ -266,7 +310,7 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
       const uint8_t *tp = wg + (int64_t)nslices * (P * 64 * PB) + t * (ntail * F::kBlockBytes);
 #pragma unroll
       for (int j = 0; j < F::kNBlk - 1; ++j)
-        if (j < ntail) lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc);
+        if (j < ntail) lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc, K);
     }
     if (t < nrows) {
 #pragma unroll
@@ -310,12 +354,12 @@ __global__ __launch_bounds__(64) void k_lmhead(const uint8_t *__restrict__ wq, c
 #pragma unroll
       for (int k = 0; k < PD; ++k) r[PD * j + k] = v[k];
     }
-    lm_slice<FMT, NB>(r, x + SE * NB * s, acc);
+    lm_slice<FMT, NB>(r, x + SE * NB * s, acc, K);
   }
   if (ntail > 0 && t < nrows) {  // rows past the vocabulary read nothing here
     const uint8_t *tp = wt + (int64_t)t * rowbytes + nmain * F::kBlockBytes;
     for (int j = 0; j < ntail; ++j)
-      lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc);
+      lm_tail_block<FMT, NB>(tp + j * F::kBlockBytes, x + 32 * NB * (nmain + j), acc, K);
   }
   if (t < nrows) {
 #pragma unroll
