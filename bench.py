@@ -90,8 +90,9 @@ WORKLOADS = {
         desc="per-row configs B=64 V=262144, rows cycle top-k 64/top-p 0.95, greedy, "
              "top-k 40/min-p 0.05, full softmax; all penalised"),
 }
+# the kernel(s) of one step: K > 64 runs as a stream launch and a per-row finish launch
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
-                   "topk128_b64": "k_topk_big_stream_vec", "topk_only_b64": "k_topk_vec",
+                   "topk128_b64": "k_topk_big_stream_vec+k_topk_big_finish_vec", "topk_only_b64": "k_topk_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec", "mixed_rows_b64": "k_topk_vec"}
 
@@ -558,24 +559,32 @@ def _counter_rows(path, counter):
 
 
 def traffic_from(workload, fetch_csv, write_csv, calib_bytes=1 << 30):
-    """Scale FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the dominant kernel
+    """Scale FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the step's kernel
     by what the same counters read for a device copy of calib_bytes, and write
-    profiles/traffic_<workload>.json."""
+    profiles/traffic_<workload>.json.  A step of several launches ("a+b")
+    adds each kernel's median dispatch."""
     kernel = DOMINANT_KERNEL[workload]
+    names = kernel.split("+")
     out = {"workload": workload, "kernel": kernel, "calibration_copy_bytes": calib_bytes,
            "algorithmic_bytes_per_launch": WORKLOADS[workload]["rows"] * WORKLOADS[workload]["vocab"] * 4}
     total = 0.0
     for counter, path, tag in (("FETCH_SIZE", fetch_csv, "fetch"), ("WRITE_SIZE", write_csv, "write")):
         rows = _counter_rows(path, counter)
-        kern = sorted(v for k, v in rows if k == kernel)
         copies = [v for k, v in rows if "copyBuffer" in k]
-        if not kern or not copies:
-            raise SystemExit(f"{path}: no {counter} rows for {kernel} or for the calibration copy")
+        meds, ndisp = [], []
+        for name in names:
+            kern = sorted(v for k, v in rows if k == name)
+            if not kern:
+                raise SystemExit(f"{path}: no {counter} rows for {name}")
+            meds.append(kern[len(kern) // 2])
+            ndisp.append(len(kern))
+        if not copies:
+            raise SystemExit(f"{path}: no {counter} rows for the calibration copy")
         calib = max(copies)  # the calib_bytes copies are the largest copy dispatches
         factor = calib_bytes / (calib * 1024.0)
-        med = kern[len(kern) // 2]
-        out[f"{tag}_kib_per_dispatch_raw"] = med
-        out[f"{tag}_dispatches"] = len(kern)
+        med = sum(meds)
+        out[f"{tag}_kib_per_dispatch_raw"] = med if len(meds) == 1 else meds
+        out[f"{tag}_dispatches"] = ndisp[0] if len(ndisp) == 1 else ndisp
         out[f"{tag}_calibration_kib_raw"] = calib
         out[f"{tag}_scale"] = factor
         out[f"{tag}_bytes_per_launch"] = med * 1024.0 * factor
