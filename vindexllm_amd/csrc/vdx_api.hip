@@ -508,13 +508,14 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   const vdx_sampler_config &c = s->cfg;
   // the paths this call takes (with per-row configs: any of the rows')
   bool path_any[4] = {false, false, false, false};
-  bool pen_fused = false, pen_sep = false, full_minp = false;
+  bool pen_fused = false, pen_sep = false, full_minp = false, slot_draw = false;
   int32_t kmax = 0, kmax_huge = 0;
   if (!s->per_row) {
     const RowCfg rc = row_params(c);
     const int path = row_path(rc, vocab);
     path_any[path] = true;
     if (path == kPathTopk) kmax = rc.top_k;
+    if (path == kPathTopk && !(rc.top_p < 1.0f)) slot_draw = true;
     if (path == kPathTopkHuge) kmax_huge = rc.top_k;
     pen_fused = row_fuses_penalty(rc, vocab);
     pen_sep = rc.penalty != 1.0f && !pen_fused;
@@ -525,6 +526,7 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
       const int path = row_path(rc, vocab);
       path_any[path] = true;
       if (path == kPathTopk && rc.top_k > kmax) kmax = rc.top_k;
+      if (path == kPathTopk && !(rc.top_p < 1.0f)) slot_draw = true;
       if (path == kPathTopkHuge && rc.top_k > kmax_huge) kmax_huge = rc.top_k;
       if (rc.penalty != 1.0f) (row_fuses_penalty(rc, vocab) ? pen_fused : pen_sep) = true;
       if (path == 2 && rc.min_p > 0.0f) full_minp = true;
@@ -586,6 +588,8 @@ int vdx_sampler_process_device(vdx_sampler *s, float *logits, int32_t rows, int3
   // empty ring), so a captured call applies it once the device fills rings.
   const bool hist = s->hist_len > 0;
   p.fuse_penalty = (hist && pen_fused) ? 1 : 0;
+  // Top-P >= 1 rows with K <= 64: slots and slot-order draw in k_topk_exact
+  p.exact_kernel = (slot_draw && cap == kCandCap) ? 1 : 0;
   const bool timed = s->timing && s->n_timed < kTimedCalls;
   hipEvent_t *ev = timed ? &s->ev[3 * s->n_timed] : nullptr;
   if (timed) HIP_TRY(s, hipEventRecord(ev[0], st));
@@ -667,6 +671,7 @@ int vdx_sample_device_noalloc(const vdx_sampler_config *cfg, float *logits, int3
   p.hist = pen ? history : nullptr;
   p.hist_len = pen ? history_stride : 0;
   p.fuse_penalty = (pen && row_fuses_penalty(rc, vocab)) ? 1 : 0;
+  p.exact_kernel = (path == kPathTopk && !(rc.top_p < 1.0f)) ? 1 : 0;
   p.rcfg = nullptr;
   p.rng.uniforms = uniforms;
   p.rng.rows = reinterpret_cast<RowState *>(ws + kNaRows);

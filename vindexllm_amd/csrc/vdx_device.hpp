@@ -239,6 +239,7 @@ struct OpMaxU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
 struct OpMinU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
 struct OpAddU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
 struct OpOrU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a | b; } };
+struct OpAddU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a + b; } };
 struct OpMaxU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
 struct OpMinU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a < b ? a : b; } };
 struct OpAddF64 {

@@ -24,6 +24,7 @@ struct CallParams {
   const int32_t *hist;  // [max_rows * hist_len]: row r's ring at hist + r * hist_len
   int32_t hist_len;     // ring stride (>= every row's window)
   int32_t fuse_penalty; // the top-K kernel applies the penalty itself
+  int32_t exact_kernel; // rows with Top-P >= 1 are finished by k_topk_exact (K <= kKMax)
   const RowCfg *rcfg;   // per-row parameters (nullptr: the fields above for every row)
   KernelRng rng;
   KernelOut out;

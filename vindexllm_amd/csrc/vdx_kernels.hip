@@ -278,6 +278,7 @@ struct TopkSmem {
   uint32_t rowflags;
   int32_t replay;
   uint32_t xw[kWaves];   // exact path: candidates per wave in the current group
+  uint64_t xw64[kWaves][4];  // exact path, whole chunk: per wave, 16 group counts in 16-bit fields
   uint32_t xmkey;        // exact path: key of the buffer's minimum
   int32_t xfrozen;       // exact path: L[0] is NaN, nothing enters
   int32_t xdone;         // exact path: the slot-order finish ran in wave 0
@@ -1521,7 +1522,7 @@ __device__ __forceinline__ void reload_chunk(const float *L, int c0, int clen, b
   }
 }
 
-template <bool VEC>
+template <bool VEC, bool WHOLE = false>
 __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const ChunkMeta *__restrict__ cm,
                                            const Cand *__restrict__ cand_row, TopkSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1598,6 +1599,68 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
     }
     // re-read the chunk and feed it one 1024-logit group at a time
     reload_chunk<VEC>(L, c0, clen, pen, v);
+    if (WHOLE && c > 0) {
+      // after chunk 0 the minimum rises slowly: the whole chunk in one list,
+      // every logit above the minimum when the chunk starts, in index order
+      // (per-thread counts of the 16 groups, four 16-bit fields per wave
+      // scan), fed in index order
+      const uint32_t m = mk;
+      uint64_t hb = 0ull;  // bit 4j + e: logit e of the thread's group j passes
+#pragma unroll
+      for (int j = 0; j < kPerThread / 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int loc = j * 1024 + wv * 256 + lane * 4 + e;
+          const float x = v[4 * j + e];
+          if (loc < clen && x == x && ord_key(x) > m) hb |= 1ull << (4 * j + e);
+        }
+      uint64_t incl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint64_t w = 0ull;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) w |= (uint64_t)__popcll((hb >> (16 * q + 4 * jj)) & 15ull) << (16 * jj);
+        incl[q] = wave_scan<uint64_t>(w, 0ull, OpAddU64());
+        if (lane == 63) sm.xw64[wv][q] = incl[q];
+      }
+      __syncthreads();
+      uint32_t gbase = 0u;
+      uint32_t off[kPerThread / 4];
+#pragma unroll
+      for (int j = 0; j < kPerThread / 4; ++j) {  // group j's offset: earlier groups, then earlier waves
+        const int q = j >> 2, sh = 16 * (j & 3);
+        uint32_t before = 0u, gt = 0u;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const uint32_t f = (uint32_t)(sm.xw64[w][q] >> sh) & 0xFFFFu;
+          before += (w < wv) ? f : 0u;
+          gt += f;
+        }
+        off[j] = gbase + before + ((uint32_t)(incl[q] >> sh) & 0xFFFFu) - (uint32_t)__popcll((hb >> (4 * j)) & 15ull);
+        gbase += gt;
+      }
+      const uint32_t total = gbase;
+      if (total <= (uint32_t)kMergeCap) {  // uniform; a longer list goes group by group, below
+#pragma unroll
+        for (int j = 0; j < kPerThread / 4; ++j) {
+          uint32_t o = off[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if ((hb >> (4 * j + e)) & 1ull)
+              list[o++] = ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(c0 + j * 1024 + wv * 256 + lane * 4 + e);
+        }
+        __syncthreads();
+        if (wv == 0) {
+          for (uint32_t g = 0u; g < total; g += 64u) {
+            const bool has = g + (uint32_t)lane < total;
+            const uint64_t en = has ? list[g + lane] : 0ull;
+            mb_feed(mb, has, (uint32_t)(en >> 32), (uint32_t)en);
+          }
+          if (lane == 0) sm.xmkey = mb.mkey;
+        }
+        continue;
+      }
+    }
     if (c == 0) {
       // the first K logits fill slots 0..K-1 (Sampler.pas:352-366); a NaN at
       // index 0 stays the minimum and nothing ever enters (:369)
@@ -1669,7 +1732,6 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   __syncthreads();
   // slot order; the running maximum M (strict '>' from L[0]): NaN when L[0]
   // is NaN, else the largest non-NaN logit, which is in the buffer
-  const bool frozen = sm.xfrozen != 0;
   if (wv == 0) {
     const uint32_t key = (uint32_t)(mb.b >> 32);
     const float x = (key == 0xFFFFFFFFu) ? __builtin_nanf("") : key_float(key);
@@ -1682,6 +1744,7 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
     if (lane == 0) sm.wfmax[0] = wm;
   }
   __syncthreads();
+  const bool frozen = sm.xfrozen != 0;
   const float M = frozen ? __builtin_nanf("") : sm.wfmax[0];
 
   // softmax over the slots (:385-391)
@@ -1861,6 +1924,7 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
                         cm + chunk, pf, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
+  if (p.exact_kernel && !(p.top_p < 1.0f)) return;  // k_topk_exact draws and finishes this row
   if (threadIdx.x == 0) {
     sm.uval = rng_draw(p.rng, row, rp);
     sm.replay = 1;
@@ -1884,6 +1948,38 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
   }
 }
+
+// Rows with Top-P >= 1 (the draw walks the min-buffer's slots, Sampler.pas:
+// 412-413, 447-459) when the call launches k_topk_exact after the top-K
+// kernel: that kernel streams their chunks (thresholds, stored candidates,
+// the fused penalty) and stops at the ticket; here one workgroup per row,
+// with the register budget of one workgroup per CU, draws u, replays the
+// buffer (a re-read chunk after chunk 0 in one index-ordered list instead of
+// 16 groups) and finishes in slot order.
+template <bool VEC>
+__device__ __forceinline__ void topk_exact_body(const CallParams &p0) {
+  __shared__ TopkSmem sm;
+  const int row = blockIdx.x;
+  if (!row_on_path(p0, row, kPathTopk)) return;
+  const CallParams p = for_row(p0, row);
+  if (p.top_p < 1.0f) return;  // finished by the top-K kernel
+  RngPre rp = rng_prefetch(p.rng, row);
+  const int S = p.nchunks;
+  const ChunkMeta *cm = p.meta + (int64_t)row * S;
+  const Cand *cr = p.cand + (int64_t)row * S * kCandCap;
+  if (threadIdx.x == 0) {
+    sm.uval = rng_draw(p.rng, row, rp);
+    sm.replay = 1;
+  }
+  __syncthreads();
+  topk_exact<VEC, true>(p, row, cm, cr, sm);
+  if (threadIdx.x == 0) {
+    p.out.tokens[row] = sm.token;
+    if (p.out.flags) p.out.flags[row] = sm.rowflags;
+  }
+}
+__global__ __launch_bounds__(kBlock) void k_topk_exact_vec(CallParams p) { topk_exact_body<true>(p); }
+__global__ __launch_bounds__(kBlock) void k_topk_exact_scalar(CallParams p) { topk_exact_body<false>(p); }
 
 // =============================================================================
 // Top-K for 64 < K <= kKBig (Sampler.pas:327-460).
@@ -3568,8 +3664,10 @@ hipError_t launch_topk(const CallParams &p, hipStream_t st) {
     }
   } else if (p.vec) {
     hipLaunchKernelGGL(k_topk_vec, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+    if (p.exact_kernel) hipLaunchKernelGGL(k_topk_exact_vec, dim3(p.rows), dim3(kBlock), 0, st, p);
   } else {
     hipLaunchKernelGGL(k_topk_scalar, grid_rows_chunks(p), dim3(kBlock), 0, st, p);
+    if (p.exact_kernel) hipLaunchKernelGGL(k_topk_exact_scalar, dim3(p.rows), dim3(kBlock), 0, st, p);
   }
   return hipGetLastError();
 }
