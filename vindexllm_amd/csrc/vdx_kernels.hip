@@ -1553,6 +1553,59 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
     const uint32_t mk = (c == 0) ? 0u : sm.xmkey;
     if (c > 0 && (sm.xfrozen || mk == 0xFFFFFFFFu)) break;  // nothing can enter any more
     const uint32_t tc = sm.ctau[c];
+    if (WHOLE && c > 0 && tc <= mk + 1u) {
+      // a run of chunks whose stored candidates hold every logit above the
+      // minimum: all of theirs above it in one index-sorted list (the minimum
+      // only rises, so a logit at or below it now never enters later)
+      int ce = c;
+      while (ce + 1 < S && ce + 1 < c + 12 && sm.ctau[ce + 1] <= mk + 1u) ++ce;  // uniform
+      if (ce > c) {
+        if (tid == 0) sm.n = 0u;
+        __syncthreads();
+        const int nitems = (ce - c + 1) * kCandCap;
+        uint64_t kk[6];
+        bool okk[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {  // every load in flight before any is used
+          const int it = tid + kBlock * i;
+          okk[i] = false;
+          kk[i] = 0ull;
+          if (it < nitems) {
+            const int cc = c + it / kCandCap, sl = it % kCandCap;
+            const uint32_t cap = (uint32_t)wave_cap(min(kChunk, V - cc * kChunk));
+            const int sh = cap == 128u ? 7 : (cap == 64u ? 6 : 5);
+            if (((uint32_t)sl & (cap - 1u)) < ((sm.ccount[cc] >> (8 * (sl >> sh))) & 0xFFu)) {
+              kk[i] = xload(&cand_row[(int64_t)cc * kCandCap + sl]);
+              okk[i] = true;
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+          if (okk[i] && (uint32_t)(kk[i] >> 32) > mk) {
+            const uint32_t q = atomicAdd(&sm.n, 1u);
+            if (q < 128u) list[q] = ((uint64_t)(~(uint32_t)kk[i]) << 32) | (kk[i] >> 32);  // index << 32 | key
+          }
+        }
+        __syncthreads();
+        const uint32_t n = sm.n;
+        if (n <= 128u) {  // uniform
+          if (wv == 0) {
+            uint64_t x[2] = {(uint32_t)lane < n ? list[lane] : ~0ull, (uint32_t)lane + 64u < n ? list[lane + 64] : ~0ull};
+            wave_sort2(x[1], x[0]);  // x[1] descending, x[0] ascending
+            const uint64_t lo = x[0] < x[1] ? x[0] : x[1], hi = x[0] < x[1] ? x[1] : x[0];
+            x[0] = wave_merge<true>(lo);
+            x[1] = wave_merge<true>(hi);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) mb_feed(mb, x[e] != ~0ull, (uint32_t)x[e], (uint32_t)(x[e] >> 32));
+            if (lane == 0) sm.xmkey = mb.mkey;
+          }
+          c = ce;
+          continue;
+        }
+        // more than one list holds: chunk c alone, below
+      }
+    }
     if (c > 0 && tc <= mk + 1u) {
       // every logit above the minimum was stored: wave 0 feeds them by index
       if (wv == 0) {
