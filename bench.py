@@ -92,7 +92,7 @@ WORKLOADS = {
 }
 # the kernel(s) of one step: K > 64 runs as a stream launch and a per-row finish launch
 DOMINANT_KERNEL = {"penalised_b64": "k_topk_vec", "topk_b256": "k_topk_vec",
-                   "topk128_b64": "k_topk_big_stream_vec+k_topk_big_finish_vec", "topk_only_b64": "k_topk_vec",
+                   "topk128_b64": "k_topk_big_stream_vec+k_topk_big_finish_vec", "topk_only_b64": "k_topk_vec+k_topk_exact_vec",
                    "full_b256": "k_full<true,false>", "greedy_b64": "k_greedy<true>",
                    "single_row": "k_topk_vec", "mixed_rows_b64": "k_topk_vec"}
 
