@@ -20,6 +20,9 @@ CASES = [
     # label, rows, vocab, config, history length (0: none)
     ("penalised B=64 V=262144", 64, 262144,
      dict(Temperature=0.8, TopK=64, TopP=0.95, RepeatPenalty=1.1, RepeatWindow=256), 256),
+    # Top-P 1: the rows finish in the second (slot-order) kernel on the same workspace
+    ("top-p 1 penalised B=16 V=262144", 16, 262144,
+     dict(Temperature=0.9, TopK=64, TopP=1.0, RepeatPenalty=1.1, RepeatWindow=64), 64),
     ("top-k 5 / min-p B=8 V=20000", 8, 20000,
      dict(Temperature=1.3, TopK=5, TopP=0.8, MinP=0.05, RepeatPenalty=1.3, RepeatWindow=16), 16),
     ("greedy B=4 V=70001", 4, 70001, dict(Temperature=0.0, RepeatPenalty=1.2, RepeatWindow=32), 20),
