@@ -293,7 +293,7 @@ struct TopkSmem {
   float v_ord[kKMax];
   // fused penalty: one entry per distinct history id, id | occurrences << 22
   uint32_t ptab[kPenHash];
-  uint64_t pbits[kBlock];  // history positions among each thread's 64 logits
+  uint32_t pcnt[8 * kBlock];  // history counts of each thread's 64 logits, 4 bits each (word-major)
   union {
     uint64_t sk[kMergeCap];
   } buf;
@@ -318,8 +318,8 @@ __device__ __forceinline__ float gmax4(const float (&v)[kPerThread], int j) {
 // (the reference mutates its input).  The ids are prefetched before the
 // chunk; while the chunk is in flight the in-chunk ids are counted in an LDS
 // open-addressing table (entry = id | occurrences << 22 over the whole
-// history) and marked in a per-thread bitmap of the positions each thread
-// holds.  Everything after (thread maxima, threshold, candidates, merge,
+// history) and each count is written, 4 bits wide, next to the logit's
+// owner thread.  Everything after (thread maxima, threshold, candidates, merge,
 // finish) then runs on penalised values, exactly as without a penalty, and
 // the stores are acknowledged before the workgroup takes its ticket, so the
 // row's last workgroup reads penalised logits wherever it re-reads the row.
@@ -328,7 +328,7 @@ static_assert(kPenPerThread == 1, "one history id per thread");
 constexpr uint32_t kPenEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kPenIdMask = (1u << 22) - 1u;  // ids < 4 Mi; count in the top 10 bits
 static_assert(kMaxChunks * kChunk <= (1 << 22) && kPenMax < 1024, "packed penalty table entries");
-static_assert(kPerThread == 64, "one bit per position of a thread in a 64-bit mask");
+static_assert(kPerThread == 64, "eight 32-bit count words of 4-bit fields per thread");
 
 struct PenaltyPrefetch {
   int cnt;
@@ -350,50 +350,23 @@ __device__ __forceinline__ uint32_t pen_hash(uint32_t id) {
 }
 static_assert(kPenHash == 1024, "pen_hash yields 10 bits");
 
-// The table and bitmap live in each kernel's shared-memory record (SM has
-// members ptab[kPenHash] and pbits[kBlock]).
+// The table and the count map live in each kernel's shared-memory record (SM
+// has members ptab[kPenHash] and pcnt[8 * kBlock]).
 struct PenaltySmem {
   uint32_t ptab[kPenHash];
-  uint64_t pbits[kBlock];  // history positions among each thread's 64 logits
+  // history occurrences of each thread's 64 logits, 4 bits each (15: 15 or
+  // more, looked up in ptab): word w of thread t at pcnt[w * kBlock + t],
+  // logit i of the thread in bits 4 (i & 7) of word i >> 3
+  uint32_t pcnt[8 * kBlock];
 };
 
-// Empties the table and the position bitmap (before a barrier).
+// Empties the table and the count map (before a barrier).
 template <class SM>
 __device__ __forceinline__ void penalty_clear(SM &sm) {
 #pragma unroll
   for (int i = 0; i < kPenHash / kBlock; ++i) sm.ptab[threadIdx.x + i * kBlock] = kPenEmpty;
-  sm.pbits[threadIdx.x] = 0ull;
-}
-
-// Counts the history ids that fall in chunk [c0, c0 + clen) (at most kPenMax
-// distinct ids in kPenHash slots, so a free slot always exists) and marks
-// their positions: bit 4j + e of sm.pbits[64 wv + lane] is position
-// chunk_pos<SPAN>(wv, lane, 4j + e), i.e. j*1024 + wv*256 + lane*4 + e in the
-// interleaved layout, wv*4096 + j*256 + lane*4 + e in the wave-span layout.
-template <bool SPAN, class SM>
-__device__ __forceinline__ void penalty_table(const CallParams &p, const PenaltyPrefetch &pf, int c0, int clen,
-                                              SM &sm) {
-  const int t = threadIdx.x;
-  const int32_t id = pf.id[0];
-  if (t < min(pf.cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
-    const uint32_t uid = (uint32_t)id;
-    uint32_t h = pen_hash(uid);
-    for (;;) {
-      const uint32_t old = atomicCAS(&sm.ptab[h], kPenEmpty, uid | (1u << 22));
-      if (old == kPenEmpty) break;
-      if ((old & kPenIdMask) == uid) {
-        atomicAdd(&sm.ptab[h], 1u << 22);
-        break;
-      }
-      h = (h + 1u) & (uint32_t)(kPenHash - 1);
-    }
-    const int pos = id - c0;
-    if (SPAN)
-      atomicOr(&sm.pbits[(pos >> 12) * 64 + ((pos >> 2) & 63)], 1ull << ((((pos >> 8) & 15) << 2) | (pos & 3)));
-    else
-      atomicOr(&sm.pbits[((pos >> 8) & 3) * 64 + ((pos >> 2) & 63)],
-               1ull << (((pos >> 10) << 2) | (pos & 3)));
-  }
+#pragma unroll
+  for (int w = 0; w < 8; ++w) sm.pcnt[w * kBlock + threadIdx.x] = 0u;
 }
 
 // Occurrences of `id` in the history (the id is in the table).
@@ -409,32 +382,76 @@ __device__ __forceinline__ uint32_t pen_count(const SM &sm, uint32_t id) {
 }
 
 // The fused penalty for one chunk whose logits are in flight into v (the
-// table was cleared at kernel start): the history ids of the chunk are
-// counted, then this thread's logits at history positions are penalised in
-// registers and in place (Sampler.pas:285-303).  Everything after runs on
-// penalised values; the stores are acknowledged before the workgroup's ticket.
+// table was cleared at kernel start).  While the chunk is in flight: the
+// history ids of the chunk are counted in the open-addressing table (at most
+// kPenMax distinct ids in kPenHash slots, so a free slot always exists), and
+// the thread that inserted each id writes its count into the count map at
+// the logit's owner (position pos is logit 4j + e of its thread:
+// j*1024 + wv*256 + lane*4 + e in the interleaved layout, wv*4096 + j*256 +
+// lane*4 + e in the wave-span layout).  Once the chunk is in, each thread
+// reads its own counts (eight words) and penalises those logits in registers
+// and in place (Sampler.pas:285-303), with no table lookup on the way.
+// Everything after runs on penalised values; the stores are acknowledged
+// before the workgroup's ticket.
 template <bool SPAN, class SM>
 __device__ __forceinline__ void penalty_pass(const CallParams &p, int row, int c0, int clen,
                                              const PenaltyPrefetch &pf, float (&v)[kPerThread], SM &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kG = kPerThread / 4;
   __syncthreads();
-  penalty_table<SPAN>(p, pf, c0, clen, sm);
+  int hs = -1;  // the table slot this thread inserted (its id's first occurrence)
+  uint32_t ow = 0u, ob = 0u;  // the logit's count word and bit
+  {
+    const int32_t id = pf.id[0];
+    if (tid < min(pf.cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
+      const uint32_t uid = (uint32_t)id;
+      uint32_t h = pen_hash(uid);
+      for (;;) {
+        const uint32_t old = atomicCAS(&sm.ptab[h], kPenEmpty, uid | (1u << 22));
+        if (old == kPenEmpty) {
+          hs = (int)h;
+          break;
+        }
+        if ((old & kPenIdMask) == uid) {
+          atomicAdd(&sm.ptab[h], 1u << 22);
+          break;
+        }
+        h = (h + 1u) & (uint32_t)(kPenHash - 1);
+      }
+      const int pos = id - c0;
+      const uint32_t t = SPAN ? (uint32_t)((pos >> 12) * 64 + ((pos >> 2) & 63))
+                              : (uint32_t)(((pos >> 8) & 3) * 64 + ((pos >> 2) & 63));
+      const uint32_t i = SPAN ? (uint32_t)((((pos >> 8) & 15) << 2) | (pos & 3))
+                              : (uint32_t)(((pos >> 10) << 2) | (pos & 3));
+      ow = (i >> 3) * kBlock + t;
+      ob = 4u * (i & 7u);
+    }
+  }
+  __syncthreads();  // the counts are final
+  if (hs >= 0) {
+    const uint32_t c = sm.ptab[hs] >> 22;
+    atomicOr(&sm.pcnt[ow], (c < 15u ? c : 15u) << ob);
+  }
   __syncthreads();
-  const uint64_t hm = sm.pbits[tid];
+  uint32_t cw[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) cw[w] = sm.pcnt[w * kBlock + tid];
+  const uint32_t any = cw[0] | cw[1] | cw[2] | cw[3] | cw[4] | cw[5] | cw[6] | cw[7];
   __builtin_amdgcn_sched_barrier(0);
-  if (__ballot(hm != 0ull)) {
+  if (__ballot(any != 0u)) {
     float *Lw = p.logits + (int64_t)row * p.stride;  // written in place: not restrict
     const double ip = 1.0 / (double)p.penalty;
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
-      const uint32_t nib = (uint32_t)(hm >> (4 * j)) & 15u;
-      if (__ballot(nib != 0u)) {
+      const uint32_t n4 = (cw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+      if (__ballot(n4 != 0u)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if ((nib >> e) & 1u) {
+          const uint32_t c = (n4 >> (4 * e)) & 15u;
+          if (c) {
             const int idx = c0 + chunk_pos<SPAN>(wv, lane, 4 * j + e);
-            const float x = penalise_fast(v[4 * j + e], (int)pen_count(sm, (uint32_t)idx), p.penalty, ip);
+            const uint32_t k = (c == 15u) ? pen_count(sm, (uint32_t)idx) : c;
+            const float x = penalise_fast(v[4 * j + e], (int)k, p.penalty, ip);
             v[4 * j + e] = x;
             xstoref(&Lw[idx], x);
           }
@@ -2057,7 +2074,7 @@ struct TopkBigSmem {
   uint32_t wflag[kWaves];
   int32_t last;
   uint32_t ptab[kPenHash];
-  uint64_t pbits[kBlock];
+  uint32_t pcnt[8 * kBlock];
   // merge
   uint32_t ctau[kMaxChunks];
   uint64_t ccnt[kMaxChunks];  // stored keys per wave region, 16 bits each
