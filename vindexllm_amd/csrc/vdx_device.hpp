@@ -341,30 +341,56 @@ __device__ __forceinline__ float u24(uint64_t x) {
 // The state one draw for `row` needs (the injected uniform, or the row's RNG
 // state), loaded by every workgroup of the row when it starts, so the one that
 // finishes the row draws without a further round trip to memory.  The state
-// was last written by an earlier launch, never by this one.
+// was last written by an earlier launch, never by this one.  It is one vector
+// load into one register (lane l < 16 holds dword l of the row's RowState,
+// lane 16 the injected uniform), not scalar loads: a wave waits for all of
+// its outstanding scalar loads at once, so a scalar load of the state (a miss
+// that queues behind the chunk loads of the workgroups already running) would
+// hold back the kernel-argument waits before this workgroup's own chunk loads.
 struct RngPre {
+  uint32_t w;
+};
+static_assert(offsetof(RowState, step) == 32 && offsetof(RowState, key) == 40 &&
+                  offsetof(RowState, ctr_row) == 60,
+              "RowState dwords read back by rng_draw");
+__device__ __forceinline__ RngPre rng_prefetch(const KernelRng &g, int row) {
+  const int l = (int)(threadIdx.x & 63u);
+  const uint32_t *a = reinterpret_cast<const uint32_t *>(&g.rows[row]) + (l & 15);
+  if (l == 16 && g.uniforms) a = reinterpret_cast<const uint32_t *>(g.uniforms + row);
+  RngPre r;
+  r.w = *a;
+  return r;
+}
+// The prefetched state read out of its register with v_readlane.  Called
+// where every lane of the wave is active (never under a per-lane condition),
+// so the load is never moved under one either: v_readlane ignores the
+// execution mask, but a lane that skipped the load holds no state.
+struct RngVals {
   uint64_t s[4];
   uint64_t step;
   uint64_t key;
   uint32_t ctr_row;
   float u;
 };
-__device__ __forceinline__ RngPre rng_prefetch(const KernelRng &g, int row) {
-  RngPre r;  // branch-free loads: the compiler can then wait for them precisely
-  const float *up = g.uniforms ? g.uniforms + row : reinterpret_cast<const float *>(&g.rows[row].step);
-  r.u = *up;
-  r.step = g.rows[row].step;
-  r.key = g.rows[row].key;
-  r.ctr_row = (uint32_t)g.rows[row].ctr_row;
-  r.s[0] = g.rows[row].rng[0];
-  r.s[1] = g.rows[row].rng[1];
-  r.s[2] = g.rows[row].rng[2];
-  r.s[3] = g.rows[row].rng[3];
-  return r;
+__device__ __forceinline__ uint64_t rng_pre64(const RngPre &r, int l) {
+  return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)r.w, l) |
+         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)r.w, l + 1) << 32);
+}
+__device__ __forceinline__ RngVals rng_unpack(const RngPre &r) {
+  RngVals v;
+  v.s[0] = rng_pre64(r, 0);
+  v.s[1] = rng_pre64(r, 2);
+  v.s[2] = rng_pre64(r, 4);
+  v.s[3] = rng_pre64(r, 6);
+  v.step = rng_pre64(r, 8);
+  v.key = rng_pre64(r, 10);
+  v.ctr_row = (uint32_t)__builtin_amdgcn_readlane((int)r.w, 15);
+  v.u = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)r.w, 16));
+  return v;
 }
 // One uniform for `row` from prefetched state: injected, or drawn (advancing
 // and storing that row's RNG).  Called by exactly one thread per row.
-__device__ __forceinline__ float rng_draw(const KernelRng &g, int row, RngPre &r) {
+__device__ __forceinline__ float rng_draw(const KernelRng &g, int row, RngVals &r) {
   float u;
   if (g.uniforms) {
     u = r.u;

@@ -338,7 +338,8 @@ struct PenaltyPrefetch {
 __device__ __forceinline__ void penalty_prefetch(const CallParams &p, int row, PenaltyPrefetch &pf) {
   const int W = p.hist_len;
   const int32_t *h = p.hist + (int64_t)row * W;
-  pf.cnt = p.rng.rows[row].hist_count;
+  // a vector load (an atomic is never a scalar load): see rng_prefetch
+  pf.cnt = __hip_atomic_load(&p.rng.rows[row].hist_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   // Unconditional load (index clamped; a position past the count is ignored
   // where the id is used), and no arithmetic on it here: the chunk's loads
   // are issued before anything waits for the id.
@@ -402,8 +403,11 @@ __device__ __forceinline__ void penalty_pass(const CallParams &p, int row, int c
   int hs = -1;  // the table slot this thread inserted (its id's first occurrence)
   uint32_t ow = 0u, ob = 0u;  // the logit's count word and bit
   {
-    const int32_t id = pf.id[0];
-    if (tid < min(pf.cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
+    // opaque from here on: a test of the prefetched values hoisted above the
+    // chunk's loads would make the wave wait for them before issuing those
+    int32_t id = pf.id[0], cnt = pf.cnt;
+    asm volatile("" : "+v"(id), "+v"(cnt));
+    if (tid < min(cnt, p.hist_len) && id >= c0 && id < c0 + clen) {
       const uint32_t uid = (uint32_t)id;
       uint32_t h = pen_hash(uid);
       for (;;) {
@@ -1985,7 +1989,7 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
   const int clen = min(kChunk, p.vocab - c0);
   ChunkMeta *cm = p.meta + (int64_t)row * S;
   Cand *cr = p.cand + (int64_t)row * S * kCandCap;
-  RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
+  RngPre rp = rng_prefetch(p.rng, row);  // one vector load, in flight with the chunk
   PenaltyPrefetch pf;
   if (p.fuse_penalty) {
     penalty_prefetch(p, row, pf);  // issued before the chunk
@@ -1995,8 +1999,9 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
                         cm + chunk, pf, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
   if (p.exact_kernel && !(p.top_p < 1.0f)) return;  // k_topk_exact draws and finishes this row
+  RngVals rv = rng_unpack(rp);
   if (threadIdx.x == 0) {
-    sm.uval = rng_draw(p.rng, row, rp);
+    sm.uval = rng_draw(p.rng, row, rv);
     sm.replay = 1;
   }
   __syncthreads();
@@ -2033,12 +2038,12 @@ __device__ __forceinline__ void topk_exact_body(const CallParams &p0) {
   if (!row_on_path(p0, row, kPathTopk)) return;
   const CallParams p = for_row(p0, row);
   if (p.top_p < 1.0f) return;  // finished by the top-K kernel
-  RngPre rp = rng_prefetch(p.rng, row);
+  RngVals rv = rng_unpack(rng_prefetch(p.rng, row));
   const int S = p.nchunks;
   const ChunkMeta *cm = p.meta + (int64_t)row * S;
   const Cand *cr = p.cand + (int64_t)row * S * kCandCap;
   if (threadIdx.x == 0) {
-    sm.uval = rng_draw(p.rng, row, rp);
+    sm.uval = rng_draw(p.rng, row, rv);
     sm.replay = 1;
   }
   __syncthreads();
@@ -2783,9 +2788,9 @@ __device__ __forceinline__ void topk_big_finish_body(const CallParams &p0) {
   const float *L = p.logits + (int64_t)row * p.stride;
   const ChunkMeta *cm = p.meta + (int64_t)row * S;
   const Cand *cr = p.cand + (int64_t)row * S * ccap;
-  RngPre rp = rng_prefetch(p.rng, row);
+  RngVals rv = rng_unpack(rng_prefetch(p.rng, row));
   if (threadIdx.x == 0) {
-    sm.uval = rng_draw(p.rng, row, rp);
+    sm.uval = rng_draw(p.rng, row, rv);
     sm.replay = 1;
   }
   __syncthreads();
@@ -2922,8 +2927,8 @@ __device__ __forceinline__ void topk_body_huge(const CallParams &p0) {
   const int G1 = (K + 63) / 64, G2 = (G1 + 63) / 64;
   const float *L = p.logits + (int64_t)row * p.stride;
   const HugeView h = huge_view(p, row, K);
-  RngPre rp = rng_prefetch(p.rng, row);
-  if (tid == 0) sm.uval = rng_draw(p.rng, row, rp);
+  RngVals rv = rng_unpack(rng_prefetch(p.rng, row));
+  if (tid == 0) sm.uval = rng_draw(p.rng, row, rv);
   uint32_t mkey = 0u, mslot = 0u;  // wave 0
   float v[kPerThread];
   const int cK = (K - 1) / kChunk;  // the chunk holding slot K-1
@@ -3266,7 +3271,7 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   FullMeta *fm = p.fmeta + (int64_t)row * S;
   const int c0 = chunk * kChunk;
   const int clen = min(kChunk, V - c0);
-  RngPre rp = rng_prefetch(p.rng, row);  // uniform loads, in flight with the chunk
+  RngPre rp = rng_prefetch(p.rng, row);  // one vector load, in flight with the chunk
   // the fused penalty (without Min-P; with it, k_full_max applied it)
   const bool pen = !EXACT && p.fuse_penalty;
   PenaltyPrefetch pf;
@@ -3363,7 +3368,8 @@ __global__ __launch_bounds__(kBlock) void k_full(CallParams p0) {
   // rescans that segment.
   if (wv == 0) {
     float u = 0.0f;
-    if (lane == 0) u = rng_draw(p.rng, row, rp);
+    RngVals rv = rng_unpack(rp);  // wave 0, every lane
+    if (lane == 0) u = rng_draw(p.rng, row, rv);
     u = __shfl(u, 0);
     // lane l holds chunks [l * per, l * per + per); each record comes in one
     // round trip
