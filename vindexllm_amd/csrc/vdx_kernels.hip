@@ -1543,9 +1543,11 @@ __device__ __forceinline__ void reload_chunk(const float *L, int c0, int clen, b
   }
 }
 
+// WHOLE (the launch of its own): the row's uniform is drawn from `rp` once
+// the buffer is final, so the state's load is in flight during the replay.
 template <bool VEC, bool WHOLE = false>
 __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const ChunkMeta *__restrict__ cm,
-                                           const Cand *__restrict__ cand_row, TopkSmem &sm) {
+                                           const Cand *__restrict__ cand_row, TopkSmem &sm, RngPre rp = {}) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int K = p.top_k, V = p.vocab, S = p.nchunks;
   const float *L = p.logits + (int64_t)row * p.stride;
@@ -1816,6 +1818,10 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
     }
     const float wm = wave_max_f32(lane < K ? x : __builtin_nanf(""));
     if (lane == 0) sm.wfmax[0] = wm;
+    if (WHOLE) {
+      RngVals rv = rng_unpack(rp);  // wave 0, every lane
+      if (lane == 0) sm.uval = rng_draw(p.rng, row, rv);
+    }
   }
   __syncthreads();
   const bool frozen = sm.xfrozen != 0;
@@ -2038,16 +2044,13 @@ __device__ __forceinline__ void topk_exact_body(const CallParams &p0) {
   if (!row_on_path(p0, row, kPathTopk)) return;
   const CallParams p = for_row(p0, row);
   if (p.top_p < 1.0f) return;  // finished by the top-K kernel
-  RngVals rv = rng_unpack(rng_prefetch(p.rng, row));
+  const RngPre rp = rng_prefetch(p.rng, row);  // drawn once the buffer is final
   const int S = p.nchunks;
   const ChunkMeta *cm = p.meta + (int64_t)row * S;
   const Cand *cr = p.cand + (int64_t)row * S * kCandCap;
-  if (threadIdx.x == 0) {
-    sm.uval = rng_draw(p.rng, row, rv);
-    sm.replay = 1;
-  }
+  if (threadIdx.x == 0) sm.replay = 1;
   __syncthreads();
-  topk_exact<VEC, true>(p, row, cm, cr, sm);
+  topk_exact<VEC, true>(p, row, cm, cr, sm, rp);
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
@@ -2788,13 +2791,16 @@ __device__ __forceinline__ void topk_big_finish_body(const CallParams &p0) {
   const float *L = p.logits + (int64_t)row * p.stride;
   const ChunkMeta *cm = p.meta + (int64_t)row * S;
   const Cand *cr = p.cand + (int64_t)row * S * ccap;
-  RngVals rv = rng_unpack(rng_prefetch(p.rng, row));
-  if (threadIdx.x == 0) {
-    sm.uval = rng_draw(p.rng, row, rv);
-    sm.replay = 1;
+  const RngPre rp = rng_prefetch(p.rng, row);  // in flight during the merge
+  if (threadIdx.x == 0) sm.replay = 1;
+  __syncthreads();
+  const bool merged = topk_merge_big<VEC>(p, L, S, cm, cr, ccap, sm);
+  {
+    RngVals rv = rng_unpack(rp);
+    if (threadIdx.x == 0) sm.uval = rng_draw(p.rng, row, rv);
   }
   __syncthreads();
-  if (topk_merge_big<VEC>(p, L, S, cm, cr, ccap, sm)) topk_finish_big(p, row, sm);
+  if (merged) topk_finish_big(p, row, sm);
   __syncthreads();
   if (sm.replay) topk_exact_big<VEC>(p, row, sm);
   if (threadIdx.x == 0) {
