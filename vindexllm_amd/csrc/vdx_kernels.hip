@@ -1552,6 +1552,17 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   const int K = p.top_k, V = p.vocab, S = p.nchunks;
   const float *L = p.logits + (int64_t)row * p.stride;
   const bool pen = p.fuse_penalty != 0;
+  float v[kPerThread];
+  // WHOLE and VEC: the chunk whose logits v holds or has in flight: chunk 0
+  // (always re-read) goes out with the records, and the next chunk is loaded
+  // while wave 0 feeds the current one's list (v is free by then); the
+  // scalar form would keep 64 loads in flight and spill
+  constexpr bool kAhead = WHOLE && VEC;
+  int vc = -1;
+  if (kAhead) {
+    reload_chunk<VEC>(L, 0, min(kChunk, V), pen, v);
+    vc = 0;
+  }
 
   // chunk records: stored counts and thresholds (an overflowed chunk is "open")
   for (int c = tid; c < S; c += kBlock) {
@@ -1567,7 +1578,6 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
   }
   MinBuf mb{~0ull, 0xFFFFFFFFu, 0u};
   uint64_t *list = sm.buf.sk;  // one group's candidates in index order: ord_key << 32 | index
-  float v[kPerThread];
   uint64_t pk0 = 0ull, pk1 = 0ull;  // wave 0: the next chunk's candidate slots, loaded ahead
   int pc = -1;                      // the chunk they belong to
   for (int c = 0; c < S; ++c) {
@@ -1674,7 +1684,7 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
       continue;
     }
     // re-read the chunk and feed it one 1024-logit group at a time
-    reload_chunk<VEC>(L, c0, clen, pen, v);
+    if (vc != c) reload_chunk<VEC>(L, c0, clen, pen, v);
     if (WHOLE && c > 0) {
       // after chunk 0 the minimum rises slowly: the whole chunk in one list,
       // every logit above the minimum when the chunk starts, in index order
@@ -1726,6 +1736,10 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
               list[o++] = ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(c0 + j * 1024 + wv * 256 + lane * 4 + e);
         }
         __syncthreads();
+        if (kAhead && c + 1 < S && sm.ctau[c + 1] > mk + 1u) {  // likely re-read next
+          reload_chunk<VEC>(L, c0 + kChunk, min(kChunk, V - c0 - kChunk), pen, v);
+          vc = c + 1;
+        }
         if (wv == 0) {
           for (uint32_t g = 0u; g < total; g += 64u) {
             const bool has = g + (uint32_t)lane < total;
@@ -1795,6 +1809,10 @@ __device__ __forceinline__ void topk_exact(const CallParams &p, int row, const C
         }
       }
       __syncthreads();
+      if (kAhead && j == kPerThread / 4 - 1 && c + 1 < S && sm.ctau[c + 1] > m + 1u) {  // likely re-read next
+        reload_chunk<VEC>(L, c0 + kChunk, min(kChunk, V - c0 - kChunk), pen, v);
+        vc = c + 1;
+      }
       if (wv == 0) {
         for (uint32_t g = 0u; g < total; g += 64u) {
           const bool has = g + (uint32_t)lane < total;
