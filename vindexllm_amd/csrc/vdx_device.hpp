@@ -68,10 +68,14 @@ __host__ __device__ __forceinline__ bool row_fuses_penalty(const RowCfg &c, int 
 // proves afterwards that the stored set holds the row's top K (theta = K-th
 // largest stored value >= every tau_c) or re-reads the chunks for which that
 // fails, so Kq may be far below K: the row's top K holds about K/S logits of
-// each of its S chunks.
-__host__ __device__ __forceinline__ int chunk_quota(int K, int S) {
+// each of its S chunks (3K/S: 12 at K = 64, S = 16, three knock-out rounds
+// per wave).  Rows whose draw walks the buffer's slots (`slots`) store four
+// more per chunk: their replay feeds a chunk from its stored keys only when
+// those include every logit above the buffer's minimum, so more stored keys
+// mean fewer chunks re-read.
+__host__ __device__ __forceinline__ int chunk_quota(int K, int S, bool slots = false) {
   if (S <= 1) return K;
-  const int q = (3 * K + S - 1) / S + 4;
+  const int q = (3 * K + S - 1) / S + (slots ? 4 : 0);
   return q < 8 ? (K < 8 ? K : 8) : (q < K ? q : K);
 }
 // The large-K kernel's quota: the row's top K holds about K/S logits of a

@@ -2019,7 +2019,7 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
     penalty_prefetch(p, row, pf);  // issued before the chunk
     penalty_clear(sm);             // ordered before the table by the stream phase's barrier
   }
-  topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S), cr + (int64_t)chunk * kCandCap,
+  topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S, p.exact_kernel && !(p.top_p < 1.0f)), cr + (int64_t)chunk * kCandCap,
                         cm + chunk, pf, sm);
   if (!last_of_row(p.tickets, row, S, &sm.last, [] {})) return;
   if (p.exact_kernel && !(p.top_p < 1.0f)) return;  // k_topk_exact draws and finishes this row
