@@ -534,7 +534,9 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p0) {
 }
 
 // `ccap`: candidate slots of a full chunk (kCandCap, or more for large K).
-template <bool VEC, class SM>
+// FASTQ: the largest quota the knock-out threshold takes (4 * kWaves per
+// round); a larger one samples thread maxima instead.
+template <bool VEC, int FASTQ = 4 * kWaves, class SM>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
                                             ChunkMeta *__restrict__ meta, const PenaltyPrefetch &pf,
@@ -556,10 +558,11 @@ __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const 
   const bool bad = hasv && !(m <= 3.4028235e38f);
   const uint32_t mk = hasv ? ord_key(m) : 0u;
   const uint64_t badw = __ballot(bad);
-  // Full chunks with a quota of at most 16: every wave finds its R-th largest
-  // thread maximum (R knock-out rounds of a wave max); tau = the smallest of
-  // the four, so >= 4R >= Kq thread maxima (distinct logits) reach tau.
-  const bool fastthr = (clen == kChunk) && Kq <= 4 * kWaves;
+  // Full chunks with a quota of at most FASTQ: every wave finds its R-th
+  // largest thread maximum (R knock-out rounds of a wave max); tau = the
+  // smallest of the four, so >= 4R >= Kq thread maxima (distinct logits)
+  // reach tau.
+  const bool fastthr = (clen == kChunk) && Kq <= FASTQ;
   if (fastthr) {
     const int R = (Kq + kWaves - 1) / kWaves;
     uint32_t key = mk, rth = 0u;
@@ -2795,7 +2798,7 @@ __device__ __forceinline__ void topk_big_stream_body(const CallParams &p0) {
     penalty_prefetch(p, row, pf);
     penalty_clear(sm);
   }
-  topk_stream<VEC>(p, row, L, c0, clen, big_chunk_quota(K, S), cr + (int64_t)chunk * ccap, cm + chunk, pf, sm,
+  topk_stream<VEC, 8 * kWaves>(p, row, L, c0, clen, big_chunk_quota(K, S), cr + (int64_t)chunk * ccap, cm + chunk, pf, sm,
                    ccap);
 }
 
