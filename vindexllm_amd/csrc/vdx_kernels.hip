@@ -305,13 +305,6 @@ __device__ __forceinline__ float gmax4(const float (&v)[kPerThread], int j) {
   return vmax(vmax(vmax(v[4 * j], v[4 * j + 1]), v[4 * j + 2]), v[4 * j + 3]);
 }
 
-// Per-chunk candidate quota.  A chunk stores every logit >= tau_c, where tau_c
-// guarantees >= Kq stored logits.  The merge proves afterwards that the stored
-// set holds the row's top K (theta = K-th largest stored value >= every tau_c)
-// or re-reads the chunks for which that fails, so Kq may be far below K: the
-// row's top 64 holds about 64/S logits of each of its S chunks.
-
-
 // Repetition penalty fused into the top-K kernel (Sampler.pas:285-303): each
 // workgroup penalises the history ids that fall in its own chunk, in its
 // registers, before it selects anything, and stores those logits in place
@@ -534,8 +527,8 @@ __global__ __launch_bounds__(kBlock) void k_greedy(CallParams p0) {
 }
 
 // `ccap`: candidate slots of a full chunk (kCandCap, or more for large K).
-// FASTQ: the largest quota the knock-out threshold takes (4 * kWaves per
-// round); a larger one samples thread maxima instead.
+// FASTQ: the largest quota the knock-out threshold takes (R = Kq / kWaves
+// rounds per wave, rounded up); a larger one samples thread maxima instead.
 template <bool VEC, int FASTQ = 4 * kWaves, class SM>
 __device__ __forceinline__ void topk_stream(const CallParams &p, int row, const float *__restrict__ L,
                                             int c0, int clen, int Kq, Cand *__restrict__ cand,
