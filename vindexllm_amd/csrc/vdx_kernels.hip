@@ -2014,6 +2014,10 @@ __device__ __forceinline__ void topk_body(const CallParams &p0) {
   if (p.fuse_penalty) {
     penalty_prefetch(p, row, pf);  // issued before the chunk
     penalty_clear(sm);             // ordered before the table by the stream phase's barrier
+    // the history ids in hand before the chunk's loads go out (issued
+    // together, they come back with the chunk under the other workgroups'
+    // loads)
+    __builtin_amdgcn_s_waitcnt(0);
   }
   topk_stream<VEC>(p, row, L, c0, clen, chunk_quota(K, S, p.exact_kernel && !(p.top_p < 1.0f)), cr + (int64_t)chunk * kCandCap,
                         cm + chunk, pf, sm);
