@@ -42,6 +42,20 @@ def test_top_p_one_walks_slots(K):
     _run(L, dict(temperature=0.8, top_k=K, top_p=1.0), u, label=f"top-p 1 K={K}")
 
 
+@pytest.mark.parametrize("V", [261144, 100000, 100003])
+def test_top_p_one_ragged_rows(V):
+    # a last chunk shorter than the rest (and, at V % 4 != 0, the scalar
+    # kernels): the replay re-reads and loads ahead chunks of every length
+    log(f"[case] top-p 1 ragged V={V}")
+    rng = np.random.default_rng(330 + V % 97)
+    B = 4
+    L = cfg1_logits(rng, B, V)
+    L[1] = np.sort(L[1])  # ascending: every logit enters, every chunk is re-read
+    u = u_stream(rng, B)
+    for K in (17, 64):
+        _run(L, dict(temperature=0.9, top_k=K, top_p=1.0), u, label=f"top-p 1 ragged V={V} K={K}")
+
+
 def test_top_p_one_penalised_batch():
     log("[case] top-p 1 penalised B=16")
     rng = np.random.default_rng(311)
