@@ -172,6 +172,21 @@ def test_topk_overflow_chunk():
     _run(L, dict(temperature=1.0, top_k=64, top_p=0.95), u, label="overflow")
 
 
+def test_topk_concentrated_in_one_chunk():
+    # the row's top K all in one chunk: that chunk's threshold is far above
+    # every other chunk's, so fewer than K stored keys reach T = max tau_c and
+    # the merge re-reads (the per-chunk quota is below K by design)
+    rng = np.random.default_rng(23)
+    B, V = 4, 262144
+    L = (rng.standard_normal((B, V))).astype(np.float32)
+    for r in range(B):
+        c = 1 + 3 * r  # a different chunk per row
+        L[r, c * 16384 + rng.choice(16384, 300, replace=False)] += np.float32(12.0)
+    u = u_stream(rng, B)
+    for K, P in ((64, 0.95), (40, 0.9), (64, 1.0)):
+        _run(L, dict(temperature=1.0, top_k=K, top_p=P), u, label=f"concentrated K={K} P={P}")
+
+
 # ----------------------------------------------------------- full path ----
 def test_cfg4_full_vocab_b256():
     rng = np.random.default_rng(1004)
