@@ -452,6 +452,40 @@ def test_rng_streams_per_row():
         assert uo.cpu().numpy()[2] == O.philox_uniform(42, 2, 0)
 
 
+@pytest.mark.parametrize("K,P", [(40, 0.9), (40, 1.0), (100, 0.9), (0, 0.9), (1500, 0.9)])
+def test_rng_streams_on_every_path(K, P):
+    # the uniform each kernel draws from its row's prefetched state (top-K
+    # fast finish, the slot-order kernel, the large-K finish, full softmax,
+    # the K > 1024 kernel): xoshiro rows equal reference samplers seeded
+    # Seed + r call for call; Philox uniforms equal the (seed, row, step)
+    # restatement
+    import torch
+    from vindexllm_amd import VDX_RNG_PHILOX, TVdxSampler
+
+    log(f"[case] rng streams K={K} P={P}")
+    rng = np.random.default_rng(77 + K)
+    B, V = 3, 5000
+    L = (2.0 * rng.standard_normal((B, V))).astype(np.float32)
+    kw = dict(temperature=1.0, top_k=K, top_p=P)
+    with TVdxSampler(0, B) as s:
+        _cfg(s, Temperature=1.0, TopK=K, TopP=P, Seed=42)
+        d = torch.from_numpy(L).cuda()
+        uo = torch.zeros(B, dtype=torch.float32, device="cuda")
+        refs = [O.Sampler() for _ in range(B)]
+        for r in range(B):
+            refs[r].set_config(O.make_config(seed=42 + r, **kw))
+        for step in range(3):
+            tok = s.process_device(d, uniforms_out=uo).cpu().numpy()
+            for r in range(B):
+                assert tok[r] == refs[r].process(L[r].copy()), (K, P, step, r)
+        s.SetRng(VDX_RNG_PHILOX)
+        for step in range(3):
+            s.process_device(d, uniforms_out=uo)
+            got = uo.cpu().numpy()
+            for r in range(B):
+                assert got[r] == O.philox_uniform(42, r, step), (K, P, step, r)
+
+
 def test_injected_u_leaves_rng_untouched():
     import torch
     from vindexllm_amd import TVdxSampler
