@@ -1464,7 +1464,9 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
 // then lowest slot; NaN sorts above +inf and is never the minimum).  A logit
 // x enters iff x > that minimum: it takes the minimum's slot, the minimum
 // leaves (lane 0), and x is inserted at its rank among the rest (lanes
-// shift down by one), i.e. one 64-bit compare, a ballot and a DPP lane shift.
+// shift down by one): lane l takes entry l + 1 if that is below x, else x if
+// its own entry is, else keeps its own (a DPP lane shift and two 64-bit
+// compares, no trip through the scalar unit).
 //
 // Only logits above the current minimum can enter, and the minimum only
 // rises, so the chunks are walked in index order: a chunk whose stored
@@ -1473,9 +1475,9 @@ __device__ __forceinline__ void topk_fast(const CallParams &p, int row, TopkSmem
 // sorted by index; any other chunk (always chunk 0) is re-read and fed one
 // 1024-logit group at a time, each group filtered against the minimum left
 // by the previous one.
-__device__ __forceinline__ uint64_t wave_shl1_64(uint64_t v) {  // lane l <- lane l + 1
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false);
+__device__ __forceinline__ uint64_t wave_shl1_64(uint64_t v) {  // lane l <- lane l + 1, lane 63 <- ~0
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false);
   return ((uint64_t)hi << 32) | lo;
 }
 constexpr uint32_t kXbIdxMask = (1u << 22) - 1u;
@@ -1493,11 +1495,10 @@ __device__ __forceinline__ void mb_refresh(MinBuf &m) {
 }
 // Logit (key xk, index xi) enters: it replaces the minimum in the minimum's slot.
 __device__ __forceinline__ void mb_enter(MinBuf &m, uint32_t xk, uint32_t xi) {
-  const uint64_t nk = ((uint64_t)xk << 32) | ((uint64_t)m.mslot << 22) | xi;
-  const int pp = __popcll(__ballot(m.b < nk) & ~1ull);  // its rank once lane 0 has left
+  // entries are distinct (each holds its slot) and nk is above lane 0's
   const uint64_t sh = wave_shl1_64(m.b);
-  const int lane = lane_id();
-  m.b = (lane < pp) ? sh : ((lane == pp) ? nk : m.b);
+  const uint64_t nk = ((uint64_t)xk << 32) | ((uint64_t)m.mslot << 22) | xi;
+  m.b = (sh < nk) ? sh : ((m.b < nk) ? nk : m.b);
   mb_refresh(m);
 }
 // One logit per lane, lane order = index order; `has` marks real entries.
