@@ -109,6 +109,26 @@ def test_nan_inf_and_signed_zero_rows():
         _run(L, dict(temperature=1.0, top_k=16, top_p=P), u, label=f"non-finite P={P}", expect_replay=False)
 
 
+def test_nan_slots_in_a_full_buffer():
+    # K = 64 with NaN slots in the fill: NaN sorts above +inf and is never the
+    # minimum, so each entering logit goes below the NaN entries, up to the
+    # highest lane that is not NaN (row 1's ramp: every one of them enters at
+    # the top; row 2: one value slot, every entry evicts it)
+    log("[case] NaN slots in a full buffer")
+    rng = np.random.default_rng(331)
+    B, V = 4, 40000
+    L = (2.0 * rng.standard_normal((B, V))).astype(np.float32)
+    L[0, [5, 17, 63]] = np.nan
+    L[1, 10:21] = np.nan
+    L[1, 64:4000] = np.linspace(-3.0, 9.0, 3936, dtype=np.float32)
+    L[2, 1:64] = np.nan
+    L[3, 40:64] = np.nan
+    L[3, 30000] = np.inf
+    u = u_stream(rng, B)
+    for P in (1.0, 0.8):
+        _run(L, dict(temperature=1.0, top_k=64, top_p=P), u, label=f"NaN slots K=64 P={P}", expect_replay=False)
+
+
 def test_exact_path_timing_b64():
     # not a bar, a record: the slot-order path on the benchmark's shape
     import torch
