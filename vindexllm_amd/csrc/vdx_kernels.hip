@@ -2547,12 +2547,40 @@ __device__ __forceinline__ void tb_enter(TourBuf &t, TopkBigSmem &sm, int K, int
   if (lane_id() == gi) t.g = gm;
   tb_refresh(t, G);
 }
-__device__ __forceinline__ void tb_feed(TourBuf &t, TopkBigSmem &sm, int K, int G, bool has, uint32_t ck,
-                                        uint32_t ci) {
+// K <= 128: the minimum from the slots' (key << 32 | slot) sorted ascending
+// over two registers of wave 0 (lanes 0-63, then 64-127; ~0 past K), an
+// entry as in the K <= 64 buffer (each position takes the next one if that is
+// below the new entry, else the new entry if its own is, else its own), the
+// shift carried from the high register's lane 0 into the low one's lane 63.
+struct SortBuf2 {
+  uint64_t lo, hi;
+};
+__device__ __forceinline__ void sb2_refresh(const SortBuf2 &b, TourBuf &t) {
+  const uint64_t m = readlane64(b.lo, 0);
+  t.mkey = (uint32_t)(m >> 32);
+  t.mslot = (uint32_t)m;
+}
+__device__ __forceinline__ void sb2_enter(SortBuf2 &b, TourBuf &t, TopkBigSmem &sm, uint32_t xk, uint32_t xi) {
+  const uint32_t s = t.mslot;
+  if (lane_id() == 0) sm.buf.x.leaf[s] = ((uint64_t)xk << 32) | xi;
+  const uint64_t nk = ((uint64_t)xk << 32) | s;
+  const uint64_t h0 = readlane64(b.hi, 0);
+  const uint64_t shl = ((uint64_t)(uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(h0 >> 32), (int)(uint32_t)(b.lo >> 32), 0x130, 0xF, 0xF, false) << 32) |
+                       (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)h0, (int)(uint32_t)b.lo, 0x130, 0xF, 0xF, false);
+  const uint64_t shh = wave_shl1_64(b.hi);
+  b.lo = (shl < nk) ? shl : ((b.lo < nk) ? nk : b.lo);
+  b.hi = (shh < nk) ? shh : ((b.hi < nk) ? nk : b.hi);
+  sb2_refresh(b, t);
+}
+__device__ __forceinline__ void tb_feed(TourBuf &t, SortBuf2 &b, bool small, TopkBigSmem &sm, int K, int G,
+                                        bool has, uint32_t ck, uint32_t ci) {
   uint64_t pend = __ballot(has && ck > t.mkey);
   while (pend) {
     const int src = __ffsll((unsigned long long)pend) - 1;
-    tb_enter(t, sm, K, G, readlane32(ck, src), readlane32(ci, src));
+    if (small)  // uniform
+      sb2_enter(b, t, sm, readlane32(ck, src), readlane32(ci, src));
+    else
+      tb_enter(t, sm, K, G, readlane32(ck, src), readlane32(ci, src));
     pend &= ~(1ull << src);
     pend &= __ballot(ck > t.mkey);
   }
@@ -2566,6 +2594,8 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
   const float *L = p.logits + (int64_t)row * p.stride;
   const bool pen = p.fuse_penalty != 0;
   TourBuf tb{~0ull, 0xFFFFFFFFu, 0u};
+  SortBuf2 sb{~0ull, ~0ull};
+  const bool small = K <= 128;
   uint64_t *list = sm.buf.x.list;
   float v[kPerThread];
   for (int c = 0; c < S; ++c) {
@@ -2582,12 +2612,22 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
         if (s < K) sm.buf.x.leaf[s] = ((uint64_t)slot_key(v[e]) << 32) | (uint32_t)s;
       }
       __syncthreads();
-      if (wv == 0) {
+      if (wv == 0 && small) {
+        // x[1] descending, x[0] ascending; lane-wise min / max are bitonic
+        uint64_t x0 = lane < K ? ((sm.buf.x.leaf[lane] & 0xFFFFFFFF00000000ull) | (uint32_t)lane) : ~0ull;
+        uint64_t x1 = lane + 64 < K ? ((sm.buf.x.leaf[lane + 64] & 0xFFFFFFFF00000000ull) | (uint32_t)(lane + 64)) : ~0ull;
+        wave_sort2(x1, x0);
+        sb.lo = wave_merge<true>(x0 < x1 ? x0 : x1);
+        sb.hi = wave_merge<true>(x0 < x1 ? x1 : x0);
+        sb2_refresh(sb, tb);
+      } else if (wv == 0) {
         for (int gi = 0; gi < G; ++gi) {
           const uint64_t gm = tb_group_min(sm, K, gi);
           if (lane == gi) tb.g = gm;
         }
         tb_refresh(tb, G);
+      }
+      if (wv == 0) {
         const float l0 = __uint_as_float(readlane32(__float_as_uint(v[0]), 0));
         if (lane == 0) {
           sm.xfrozen = (l0 != l0) ? 1 : 0;
@@ -2628,7 +2668,7 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
         for (uint32_t g = 0u; g < total; g += 64u) {
           const bool has = g + (uint32_t)lane < total;
           const uint64_t en = has ? list[g + lane] : 0ull;
-          tb_feed(tb, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
+          tb_feed(tb, sb, small, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
         }
         if (lane == 0) sm.xmkey = tb.mkey;
       }
