@@ -93,6 +93,26 @@ def test_large_k_nonfinite():
         _run(L, dict(temperature=1.0, top_k=300, top_p=P), u, label=f"non-finite P={P}")
 
 
+@pytest.mark.parametrize("K", [70, 128])
+def test_large_k_nan_slots_two_registers(K):
+    # K <= 128 keeps the slot-order buffer sorted over two registers: NaN
+    # slots at its top, entries below them up to the highest lane that is
+    # not NaN (row 1's ramp: each one enters at the top), the shift carried
+    # across the two registers
+    log(f"[case] large K NaN slots K={K}")
+    rng = np.random.default_rng(441 + K)
+    B, V = 4, 40000
+    L = (2.0 * rng.standard_normal((B, V))).astype(np.float32)
+    L[0, [5, 66, K - 1]] = np.nan
+    L[1, 60:69] = np.nan
+    L[1, K:K + 3000] = np.linspace(-3.0, 9.0, 3000, dtype=np.float32)
+    L[2, 1:K] = np.nan
+    L[3, 30000] = np.inf
+    u = u_stream(rng, B)
+    for P in (1.0, 0.85):
+        _run(L, dict(temperature=1.0, top_k=K, top_p=P), u, label=f"NaN slots K={K} P={P}")
+
+
 def test_rows_of_several_k_in_one_call():
     # per-row configs: K <= 64 and K > 64 rows sampled together
     import torch
