@@ -2121,6 +2121,7 @@ struct TopkBigSmem {
   double wtot[kWaves];
   double S;
   // exact path
+  uint64_t xw64[kWaves][4];  // exact path: per-wave group counts of a whole chunk
   uint32_t xw[kWaves];
   uint32_t xmkey;
   int32_t xfrozen;
@@ -2633,6 +2634,68 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
           sm.xfrozen = (l0 != l0) ? 1 : 0;
           sm.xmkey = tb.mkey;
         }
+      }
+    }
+    if (c > 0) {
+      // after chunk 0 the minimum rises slowly: every logit above it when the
+      // chunk starts in one index-ordered list (per-thread counts of the 16
+      // groups, four 16-bit fields per wave scan), fed in index order; a
+      // longer list goes group by group, below
+      const uint32_t m = sm.xmkey;
+      uint64_t hb = 0ull;  // bit 4j + e: logit e of the thread's group j passes
+#pragma unroll
+      for (int j = 0; j < kPerThread / 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int loc = j * 1024 + wv * 256 + lane * 4 + e;
+          const float x = v[4 * j + e];
+          if (loc < clen && x == x && ord_key(x) > m) hb |= 1ull << (4 * j + e);
+        }
+      uint64_t incl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint64_t w = 0ull;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) w |= (uint64_t)__popcll((hb >> (16 * q + 4 * jj)) & 15ull) << (16 * jj);
+        incl[q] = wave_scan<uint64_t>(w, 0ull, OpAddU64());
+        if (lane == 63) sm.xw64[wv][q] = incl[q];
+      }
+      __syncthreads();
+      uint32_t gbase = 0u;
+      uint32_t off[kPerThread / 4];
+#pragma unroll
+      for (int j = 0; j < kPerThread / 4; ++j) {  // group j's offset: earlier groups, then earlier waves
+        const int q = j >> 2, sh = 16 * (j & 3);
+        uint32_t before = 0u, gt = 0u;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const uint32_t f = (uint32_t)(sm.xw64[w][q] >> sh) & 0xFFFFu;
+          before += (w < wv) ? f : 0u;
+          gt += f;
+        }
+        off[j] = gbase + before + ((uint32_t)(incl[q] >> sh) & 0xFFFFu) - (uint32_t)__popcll((hb >> (4 * j)) & 15ull);
+        gbase += gt;
+      }
+      const uint32_t total = gbase;
+      if (total <= 1024u) {  // uniform
+#pragma unroll
+        for (int j = 0; j < kPerThread / 4; ++j) {
+          uint32_t o = off[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if ((hb >> (4 * j + e)) & 1ull)
+              list[o++] = ((uint64_t)ord_key(v[4 * j + e]) << 32) | (uint32_t)(c0 + j * 1024 + wv * 256 + lane * 4 + e);
+        }
+        __syncthreads();
+        if (wv == 0) {
+          for (uint32_t g = 0u; g < total; g += 64u) {
+            const bool has = g + (uint32_t)lane < total;
+            const uint64_t en = has ? list[g + lane] : 0ull;
+            tb_feed(tb, sb, small, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
+          }
+          if (lane == 0) sm.xmkey = tb.mkey;
+        }
+        continue;
       }
     }
 #pragma unroll
