@@ -2573,13 +2573,40 @@ __device__ __forceinline__ void sb2_enter(SortBuf2 &b, TourBuf &t, TopkBigSmem &
   b.hi = (shh < nk) ? shh : ((b.hi < nk) ? nk : b.hi);
   sb2_refresh(b, t);
 }
-__device__ __forceinline__ void tb_feed(TourBuf &t, SortBuf2 &b, bool small, TopkBigSmem &sm, int K, int G,
+// 128 < K <= 256: the same over four registers (positions 64i + lane of
+// register i), each register's lane 63 taking the next one's lane 0.
+struct SortBuf4 {
+  uint64_t r[4];
+};
+__device__ __forceinline__ uint64_t shl1_from(uint64_t v, uint64_t in63) {  // lane l <- lane l + 1, lane 63 <- in63
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(in63 >> 32), (int)(uint32_t)(v >> 32), 0x130, 0xF, 0xF, false) << 32) |
+         (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)in63, (int)(uint32_t)v, 0x130, 0xF, 0xF, false);
+}
+__device__ __forceinline__ void sb4_enter(SortBuf4 &b, TourBuf &t, TopkBigSmem &sm, uint32_t xk, uint32_t xi) {
+  const uint32_t s = t.mslot;
+  if (lane_id() == 0) sm.buf.x.leaf[s] = ((uint64_t)xk << 32) | xi;
+  const uint64_t nk = ((uint64_t)xk << 32) | s;
+  const uint64_t c0 = readlane64(b.r[1], 0), c1 = readlane64(b.r[2], 0), c2 = readlane64(b.r[3], 0);
+  const uint64_t s0 = shl1_from(b.r[0], c0), s1 = shl1_from(b.r[1], c1), s2 = shl1_from(b.r[2], c2),
+                 s3 = shl1_from(b.r[3], ~0ull);
+  b.r[0] = (s0 < nk) ? s0 : ((b.r[0] < nk) ? nk : b.r[0]);
+  b.r[1] = (s1 < nk) ? s1 : ((b.r[1] < nk) ? nk : b.r[1]);
+  b.r[2] = (s2 < nk) ? s2 : ((b.r[2] < nk) ? nk : b.r[2]);
+  b.r[3] = (s3 < nk) ? s3 : ((b.r[3] < nk) ? nk : b.r[3]);
+  const uint64_t m = readlane64(b.r[0], 0);
+  t.mkey = (uint32_t)(m >> 32);
+  t.mslot = (uint32_t)m;
+}
+template <int MODE>
+__device__ __forceinline__ void tb_feed(TourBuf &t, SortBuf2 &b, SortBuf4 &b4, TopkBigSmem &sm, int K, int G,
                                         bool has, uint32_t ck, uint32_t ci) {
   uint64_t pend = __ballot(has && ck > t.mkey);
   while (pend) {
     const int src = __ffsll((unsigned long long)pend) - 1;
-    if (small)  // uniform
+    if constexpr (MODE == 2)
       sb2_enter(b, t, sm, readlane32(ck, src), readlane32(ci, src));
+    else if constexpr (MODE == 4)
+      sb4_enter(b4, t, sm, readlane32(ck, src), readlane32(ci, src));
     else
       tb_enter(t, sm, K, G, readlane32(ck, src), readlane32(ci, src));
     pend &= ~(1ull << src);
@@ -2587,7 +2614,9 @@ __device__ __forceinline__ void tb_feed(TourBuf &t, SortBuf2 &b, bool small, Top
   }
 }
 
-template <bool VEC>
+// MODE: the buffer's minimum from 2 or 4 sorted registers (K <= 128, <= 256)
+// or the tournament (0); one instantiation each, so each keeps its registers
+template <bool VEC, int MODE>
 __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, TopkBigSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int K = p.top_k, V = p.vocab, S = p.nchunks;
@@ -2596,7 +2625,9 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
   const bool pen = p.fuse_penalty != 0;
   TourBuf tb{~0ull, 0xFFFFFFFFu, 0u};
   SortBuf2 sb{~0ull, ~0ull};
-  const bool small = K <= 128;
+  SortBuf4 sb4{{~0ull, ~0ull, ~0ull, ~0ull}};
+  constexpr bool small = MODE == 2;
+  constexpr int mode = MODE;
   uint64_t *list = sm.buf.x.list;
   float v[kPerThread];
   for (int c = 0; c < S; ++c) {
@@ -2621,6 +2652,23 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
         sb.lo = wave_merge<true>(x0 < x1 ? x0 : x1);
         sb.hi = wave_merge<true>(x0 < x1 ? x1 : x0);
         sb2_refresh(sb, tb);
+      } else if (mode == 4) {
+        // entry (key << 32 | slot) of slot s at its rank among the K
+        if (tid < K) {
+          const uint64_t e = (sm.buf.x.leaf[tid] & 0xFFFFFFFF00000000ull) | (uint32_t)tid;
+          uint32_t rk = 0u;
+          for (int t2 = 0; t2 < K; ++t2)
+            rk += (((sm.buf.x.leaf[t2] & 0xFFFFFFFF00000000ull) | (uint32_t)t2) < e) ? 1u : 0u;
+          list[rk] = e;
+        }
+        __syncthreads();
+        if (wv == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sb4.r[i] = (64 * i + lane < K) ? list[64 * i + lane] : ~0ull;
+          const uint64_t m = readlane64(sb4.r[0], 0);
+          tb.mkey = (uint32_t)(m >> 32);
+          tb.mslot = (uint32_t)m;
+        }
       } else if (wv == 0) {
         for (int gi = 0; gi < G; ++gi) {
           const uint64_t gm = tb_group_min(sm, K, gi);
@@ -2691,7 +2739,7 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
           for (uint32_t g = 0u; g < total; g += 64u) {
             const bool has = g + (uint32_t)lane < total;
             const uint64_t en = has ? list[g + lane] : 0ull;
-            tb_feed(tb, sb, small, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
+            tb_feed<MODE>(tb, sb, sb4, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
           }
           if (lane == 0) sm.xmkey = tb.mkey;
         }
@@ -2731,7 +2779,7 @@ __device__ __forceinline__ void topk_exact_big(const CallParams &p, int row, Top
         for (uint32_t g = 0u; g < total; g += 64u) {
           const bool has = g + (uint32_t)lane < total;
           const uint64_t en = has ? list[g + lane] : 0ull;
-          tb_feed(tb, sb, small, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
+          tb_feed<MODE>(tb, sb, sb4, sm, K, G, has, (uint32_t)(en >> 32), (uint32_t)en);
         }
         if (lane == 0) sm.xmkey = tb.mkey;
       }
@@ -2924,7 +2972,14 @@ __device__ __forceinline__ void topk_big_finish_body(const CallParams &p0) {
   __syncthreads();
   if (merged) topk_finish_big(p, row, sm);
   __syncthreads();
-  if (sm.replay) topk_exact_big<VEC>(p, row, sm);
+  if (sm.replay) {
+    if (p.top_k <= 128)
+      topk_exact_big<VEC, 2>(p, row, sm);
+    else if (p.top_k <= 256)
+      topk_exact_big<VEC, 4>(p, row, sm);
+    else
+      topk_exact_big<VEC, 0>(p, row, sm);
+  }
   if (threadIdx.x == 0) {
     p.out.tokens[row] = sm.token;
     if (p.out.flags) p.out.flags[row] = sm.rowflags;
