@@ -3,8 +3,8 @@
 The reference takes any 0 < TopK < V (Sampler.pas:327-383, the min-buffer
 sized to K at :334).  Rows with K > 64 run the large-K kernel: more candidate
 slots per chunk, an LDS radix select with chunk re-reads, a workgroup-wide
-sort and finish, and for the exact slot-order replay a buffer sorted over two
-or four registers (K <= 128, <= 256) or a tournament (larger K).
+sort and finish, and for the exact slot-order replay a buffer sorted over 2
+or 4 registers (K <= 128, <= 256) or a tournament (larger K).
 Tokens, top-K sets (in value order) and final probabilities are compared to
 the oracle at the sampler's bar on the benchmark's vocabulary, for Top-P
 below and at 1 (the draw then walks the reference's slot order), integer
@@ -94,12 +94,12 @@ def test_large_k_nonfinite():
         _run(L, dict(temperature=1.0, top_k=300, top_p=P), u, label=f"non-finite P={P}")
 
 
-@pytest.mark.parametrize("K", [70, 128, 129, 200, 256])
+@pytest.mark.parametrize("K", [70, 128, 129, 200, 256, 300])
 def test_large_k_nan_slots_sorted_registers(K):
-    # K <= 256 keeps the slot-order buffer sorted over two or four registers:
-    # NaN slots at its top, entries below them up to the highest lane that is
-    # not NaN (row 1's ramp: each one enters at the top), the shift carried
-    # from register to register
+    # K <= 256 keeps the slot-order buffer sorted over 2 or 4 registers
+    # (K = 300: the tournament): NaN slots at its top, entries below them up
+    # to the highest lane that is not NaN (row 1's ramp: each one enters at
+    # the top), the shift carried from register to register
     log(f"[case] large K NaN slots K={K}")
     rng = np.random.default_rng(441 + K)
     B, V = 4, 40000
